@@ -1,0 +1,110 @@
+/*
+ * ttk_hip.h - C ABI of the MI355X (gfx950) fused attention and fused
+ * residual-add + LayerNorm kernels.
+ *
+ * Plain C: no HIP, no torch types.  Every tensor is a raw device pointer plus
+ * element strides.  The caller owns all memory (inputs and outputs); the
+ * library never allocates, frees, retains a pointer past the call, or
+ * synchronises.  Each call enqueues its kernel(s) on `stream` (a hipStream_t
+ * passed as void*; NULL is the legacy default stream), so calls are legal
+ * inside hipGraph stream capture.
+ *
+ * Errors: every entry point returns a ttk_status.  On failure the message is
+ * available from ttk_last_error() on the calling thread (thread-local).  No
+ * entry point falls back to another implementation.
+ *
+ * Library: libttk_hip.so, built by triton-transformer-kernels_amd/build.py.
+ */
+#ifndef TTK_HIP_H
+#define TTK_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTK_ABI_VERSION 1
+
+typedef enum {
+  TTK_OK = 0,
+  TTK_EINVAL = 1,       /* malformed arguments: null pointer, bad size/stride */
+  TTK_EUNSUPPORTED = 2, /* well-formed but outside the kernels' envelope     */
+  TTK_ELAUNCH = 3       /* the HIP runtime rejected the launch               */
+} ttk_status;
+
+typedef enum { TTK_F32 = 0, TTK_BF16 = 1, TTK_F16 = 2 } ttk_dtype;
+
+/* Version of this ABI (TTK_ABI_VERSION of the built library). */
+int ttk_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ttk_last_error(void);
+
+/*
+ * Fused forward attention over the [B, S, H, D] ("BSHD") layout:
+ *
+ *   out[b,s,h,:] = sum_t P[s,t] * v[b,t,h,:],
+ *   P[s,:] = softmax_t( scale * <q[b,s,h,:], k[b,t,h,:]> ) over allowed t,
+ *   allowed(s,t) = key_valid[b,t] (if given) && (!causal || t <= s).
+ *
+ * Softmax statistics and the output accumulator are fp32; the score matrix is
+ * never materialised.  A query row with no allowed key produces exact zeros.
+ * Causal launches never visit key tiles past the query tile's diagonal.
+ *
+ * q/k/v/out: device pointers of dtype `dtype` (TTK_F32, TTK_BF16, TTK_F16).
+ * *_strides[3]: element strides of the B, S and H axes; the D axis has
+ *   stride 1.  Rows must be 16-byte aligned (pointer and every stride times
+ *   the element size a multiple of 16 bytes) - otherwise TTK_EUNSUPPORTED.
+ * key_valid: NULL, or a [B, S] byte mask (nonzero = valid) with element
+ *   strides mask_strides[2] (mask_strides may be NULL when key_valid is).
+ * D must be one of 8, 16, 32, 64, 128.
+ *
+ * Replaces the launch of `_attention_fwd` inside `triton_attention`
+ * (reference transformer_opt/kernels/attention.py:268-360, kernel :103-265);
+ * the argument meaning (BSHD strides, optional [B,S] key mask, causal flag,
+ * softmax scale) is that launch's.
+ */
+ttk_status ttk_attention_fwd(const void* q, const void* k, const void* v,
+                             const uint8_t* key_valid, void* out, int dtype,
+                             int64_t B, int64_t S, int64_t H, int64_t D,
+                             const int64_t q_strides[3],
+                             const int64_t k_strides[3],
+                             const int64_t v_strides[3],
+                             const int64_t mask_strides[2],
+                             const int64_t o_strides[3], float scale,
+                             int causal, void* stream);
+
+/*
+ * Fused residual add + LayerNorm over `rows` contiguous rows of width N:
+ *
+ *   r = x + u                        (u == NULL means r = x)
+ *   if zero_invalid_residual:   r[row] = 0 where row_valid[row] == 0
+ *   y = (r - mean(r)) * rsqrt(var(r) + eps) * w + b   (biased variance)
+ *   if zero_invalid_normalized: y[row] = 0 where row_valid[row] == 0
+ *
+ * Writes r to residual_out (skipped when residual_out == NULL) and y to
+ * normalized_out.  Statistics are fp32; r is rounded to `dtype` before the
+ * statistics are taken, exactly as an eager `x + u` followed by a LayerNorm.
+ * x, u, residual_out, normalized_out: rows*N contiguous elements of `dtype`;
+ * w: N elements; b: N elements or NULL; row_valid: `rows` bytes or NULL
+ * (required when either zeroing flag is set).
+ *
+ * Replaces the launch of `_residual_layer_norm_fwd` inside
+ * `fused_residual_layer_norm` (reference
+ * transformer_opt/kernels/residual_layer_norm.py:159-237, kernel :73-126).
+ */
+ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u,
+                                      const void* w, const void* b,
+                                      const uint8_t* row_valid,
+                                      void* residual_out, void* normalized_out,
+                                      int dtype, int64_t rows, int64_t N,
+                                      float eps, int zero_invalid_residual,
+                                      int zero_invalid_normalized,
+                                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTK_HIP_H */

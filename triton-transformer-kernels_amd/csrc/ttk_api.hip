@@ -1,0 +1,204 @@
+// C ABI of libttk_hip.so: argument validation and kernel dispatch.
+//
+// The entry points validate everything the kernels assume (non-null
+// pointers, positive sizes, 16-byte row alignment, supported head dims and
+// dtypes) BEFORE any HIP call, so a rejected call touches no device state.
+// They never allocate, free, synchronise or keep pointers; the kernels are
+// enqueued on the caller's stream, which keeps every call capturable in a
+// hipGraph.  The only global state is the thread-local error message.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <limits>
+
+#include "ttk_common.h"
+#include "ttk_hip.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+ttk_status fail(ttk_status status, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, args);
+  va_end(args);
+  return status;
+}
+
+int elem_bytes(int dtype) {
+  switch (dtype) {
+    case TTK_F32: return 4;
+    case TTK_BF16: return 2;
+    case TTK_F16: return 2;
+    default: return 0;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int64_t kIntMax = std::numeric_limits<int>::max();
+
+}  // namespace
+
+extern "C" int ttk_abi_version(void) { return TTK_ABI_VERSION; }
+
+extern "C" const char* ttk_last_error(void) { return g_error; }
+
+extern "C" ttk_status ttk_attention_fwd(const void* q, const void* k, const void* v,
+                                        const uint8_t* key_valid, void* out, int dtype,
+                                        int64_t B, int64_t S, int64_t H, int64_t D,
+                                        const int64_t q_strides[3], const int64_t k_strides[3],
+                                        const int64_t v_strides[3], const int64_t mask_strides[2],
+                                        const int64_t o_strides[3], float scale, int causal,
+                                        void* stream) {
+  g_error[0] = '\0';
+  const int es = elem_bytes(dtype);
+  if (es == 0) return fail(TTK_EUNSUPPORTED, "attention: unsupported dtype code %d", dtype);
+  if (B < 0 || S <= 0 || H <= 0 || D <= 0) {
+    return fail(TTK_EINVAL,
+                "attention: sequence length, head count, and head dimension must be positive "
+                "(B=%lld S=%lld H=%lld D=%lld)",
+                (long long)B, (long long)S, (long long)H, (long long)D);
+  }
+  if (D != 8 && D != 16 && D != 32 && D != 64 && D != 128) {
+    return fail(TTK_EUNSUPPORTED, "attention: head_dim=%lld is outside [8, 16, 32, 64, 128]",
+                (long long)D);
+  }
+  if (!q_strides || !k_strides || !v_strides || !o_strides) {
+    return fail(TTK_EINVAL, "attention: stride arrays must not be NULL");
+  }
+  if (key_valid != nullptr && mask_strides == nullptr) {
+    return fail(TTK_EINVAL, "attention: key_valid given without mask_strides");
+  }
+  if (B == 0) return TTK_OK;  // empty batch: nothing to launch
+  if (!q || !k || !v || !out) return fail(TTK_EINVAL, "attention: q, k, v and out must not be NULL");
+  if (S > (int64_t{1} << 24)) {
+    return fail(TTK_EUNSUPPORTED, "attention: seq_len=%lld exceeds the kernel limit %d",
+                (long long)S, 1 << 24);
+  }
+  const int64_t bm = ttk::attention_block_m(dtype, static_cast<int>(D));
+  const int64_t nq = (S + bm - 1) / bm;
+  if (B * H > kIntMax / nq) return fail(TTK_EUNSUPPORTED, "attention: grid too large");
+  const void* ptrs[4] = {q, k, v, out};
+  const int64_t* strides[4] = {q_strides, k_strides, v_strides, o_strides};
+  const char* names[4] = {"q", "k", "v", "out"};
+  for (int i = 0; i < 4; ++i) {
+    if (!aligned16(ptrs[i])) {
+      return fail(TTK_EUNSUPPORTED, "attention: %s is not 16-byte aligned", names[i]);
+    }
+    for (int a = 0; a < 3; ++a) {
+      if (strides[i][a] < 0 || (strides[i][a] * es) % 16 != 0) {
+        return fail(TTK_EUNSUPPORTED,
+                    "attention: %s stride[%d]=%lld is not a non-negative multiple of 16 bytes",
+                    names[i], a, (long long)strides[i][a]);
+      }
+    }
+  }
+  if (key_valid != nullptr && (mask_strides[0] < 0 || mask_strides[1] < 0)) {
+    return fail(TTK_EINVAL, "attention: mask strides must be non-negative");
+  }
+
+  ttk::AttnParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.mask = key_valid;
+  p.out = out;
+  p.qb = q_strides[0]; p.qs = q_strides[1]; p.qh = q_strides[2];
+  p.kb = k_strides[0]; p.ks = k_strides[1]; p.kh = k_strides[2];
+  p.vb = v_strides[0]; p.vs = v_strides[1]; p.vh = v_strides[2];
+  p.ob = o_strides[0]; p.os = o_strides[1]; p.oh = o_strides[2];
+  p.mb = key_valid ? mask_strides[0] : 0;
+  p.ms = key_valid ? mask_strides[1] : 0;
+  p.S = static_cast<int>(S);
+  p.H = static_cast<int>(H);
+  p.BH = static_cast<int>(B * H);
+  p.nq = static_cast<int>(nq);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.xcd_swizzle = (p.BH % 8 == 0) ? 1 : 0;
+  const int grid = static_cast<int>(nq * B * H);
+
+  const hipError_t err = ttk::launch_attention(dtype, static_cast<int>(D), causal != 0,
+                                               key_valid != nullptr, p, grid,
+                                               static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    return fail(TTK_ELAUNCH, "attention: launch failed: %s", hipGetErrorString(err));
+  }
+  return TTK_OK;
+}
+
+extern "C" ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u, const void* w,
+                                                 const void* b, const uint8_t* row_valid,
+                                                 void* residual_out, void* normalized_out,
+                                                 int dtype, int64_t rows, int64_t N, float eps,
+                                                 int zero_invalid_residual,
+                                                 int zero_invalid_normalized, void* stream) {
+  g_error[0] = '\0';
+  const int es = elem_bytes(dtype);
+  if (es == 0) return fail(TTK_EUNSUPPORTED, "layernorm: unsupported dtype code %d", dtype);
+  if (rows < 0 || N <= 0) {
+    return fail(TTK_EINVAL, "layernorm: rows must be >= 0 and N > 0 (rows=%lld N=%lld)",
+                (long long)rows, (long long)N);
+  }
+  if (N > 65536) {
+    return fail(TTK_EUNSUPPORTED,
+                "layernorm: normalized feature dimension %lld exceeds the fused kernel limit 65536",
+                (long long)N);
+  }
+  if ((zero_invalid_residual || zero_invalid_normalized) && row_valid == nullptr) {
+    return fail(TTK_EINVAL, "layernorm: invalid-row zeroing requires valid_token_mask");
+  }
+  if (rows == 0) return TTK_OK;
+  if (!x || !w || !normalized_out) {
+    return fail(TTK_EINVAL, "layernorm: x, weight and normalized_out must not be NULL");
+  }
+  if (rows > kIntMax) return fail(TTK_EUNSUPPORTED, "layernorm: too many rows (%lld)", (long long)rows);
+
+  ttk::LnParams p{};
+  p.x = x;
+  p.u = u;
+  p.w = w;
+  p.b = b;
+  p.valid = row_valid;
+  p.r_out = residual_out;
+  p.y_out = normalized_out;
+  p.rows = rows;
+  p.N = static_cast<int>(N);
+  p.eps = eps;
+  p.zero_res = zero_invalid_residual ? 1 : 0;
+  p.zero_norm = zero_invalid_normalized ? 1 : 0;
+
+  // Register-resident vector path: whole 16-byte vectors, aligned tensors,
+  // at most 16 vectors per lane.
+  const int vn = 16 / es;
+  bool vector_path = (N % vn) == 0;
+  for (const void* ptr : {x, u, w, b, static_cast<const void*>(residual_out),
+                          static_cast<const void*>(normalized_out)}) {
+    if (ptr != nullptr && !aligned16(ptr)) vector_path = false;
+  }
+  int vpl = 0;
+  if (vector_path) {
+    const int64_t nv = N / vn;
+    int lpr = 1;
+    while (lpr < 64 && nv % (2 * lpr) == 0) lpr *= 2;
+    int64_t per_lane = nv / lpr;
+    // Narrow rows: several rows per wavefront, >= 4 vectors per lane.
+    while (per_lane < 4 && lpr > 8) {
+      lpr /= 2;
+      per_lane *= 2;
+    }
+    if (per_lane > 16) {
+      vector_path = false;
+    } else {
+      p.lanes_per_row = lpr;
+      vpl = static_cast<int>(per_lane);
+    }
+  }
+  const hipError_t err = ttk::launch_residual_layernorm(dtype, p, vector_path, vpl,
+                                                        static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    return fail(TTK_ELAUNCH, "layernorm: launch failed: %s", hipGetErrorString(err));
+  }
+  return TTK_OK;
+}

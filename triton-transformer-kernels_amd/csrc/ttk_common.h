@@ -1,0 +1,99 @@
+// Shared definitions of the gfx950 kernels and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace ttk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Storage tags.  Device code moves 16-bit types as raw ushort bits and
+// converts explicitly, so the numerics never depend on header operators.
+struct F32 {
+  using storage = float;
+  static constexpr int kBytes = 4;
+};
+struct BF16 {
+  using storage = unsigned short;
+  static constexpr int kBytes = 2;
+};
+struct F16 {
+  using storage = unsigned short;
+  static constexpr int kBytes = 2;
+};
+
+__device__ __forceinline__ float to_f32(F32, float v) { return v; }
+__device__ __forceinline__ float to_f32(BF16, unsigned short v) {
+  return __uint_as_float(static_cast<unsigned int>(v) << 16);
+}
+__device__ __forceinline__ float to_f32(F16, unsigned short v) {
+  _Float16 h = __builtin_bit_cast(_Float16, v);
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ float from_f32(F32, float v) { return v; }
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN), the rounding torch uses.
+__device__ __forceinline__ unsigned short from_f32(BF16, float v) {
+  unsigned int u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<unsigned short>(u >> 16);
+}
+__device__ __forceinline__ unsigned short from_f32(F16, float v) {
+  _Float16 h = static_cast<_Float16>(v);  // v_cvt_f16_f32: round to nearest even
+  return __builtin_bit_cast(unsigned short, h);
+}
+
+// Launch parameters of the attention kernels (element strides).
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const uint8_t* mask;
+  void* out;
+  int64_t qb, qs, qh;
+  int64_t kb, ks, kh;
+  int64_t vb, vs, vh;
+  int64_t mb, ms;
+  int64_t ob, os, oh;
+  int S, H, BH, nq;
+  float scale_log2;  // softmax scale * log2(e)
+  int xcd_swizzle;   // 1 when BH % 8 == 0: heads are pinned to XCDs
+};
+
+// Launch parameters of the residual + LayerNorm kernels.
+struct LnParams {
+  const void* x;
+  const void* u;
+  const void* w;
+  const void* b;
+  const uint8_t* valid;
+  void* r_out;
+  void* y_out;
+  int64_t rows;
+  int N;
+  int lanes_per_row;  // vector kernel: lanes that share one row (power of 2)
+  float eps;
+  int zero_res;
+  int zero_norm;
+};
+
+// Host-side launchers (defined next to their kernels).  Return a HIP error.
+hipError_t launch_attention(int dtype, int D, bool causal, bool has_mask,
+                            const AttnParams& p, int grid, hipStream_t stream);
+int attention_block_m(int dtype, int D);
+
+hipError_t launch_residual_layernorm(int dtype, const LnParams& p, bool vector_path,
+                                     int vectors_per_lane, hipStream_t stream);
+
+}  // namespace ttk

@@ -1,0 +1,65 @@
+"""Auditable attention dispatch onto the gfx950 HIP kernel.
+
+Mirrors the reference's ``transformer_opt/dispatch.py``: the same
+``attention_forward(q, k, v, valid_token_mask, *, causal, scale, backend)``
+signature returning ``(output, AttentionDispatch(requested, selected,
+reason))`` and the same exception contract - an unknown backend is a
+``ValueError`` (dispatch.py:26-30), a forced backend that cannot run is a
+``RuntimeError`` when the hardware path is absent (dispatch.py:120-121) and a
+``ValueError`` when the inputs are unsupported (dispatch.py:122-123).
+
+Unlike the reference there is no SDPA or explicit-math route (dispatch.py:
+33-96, 145-161): ``auto`` selects the HIP kernel or raises with the support
+reason.  The explicit reference attention lives only in the test oracle.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from .config import ATTENTION_BACKENDS, hip_attention_support
+from .kernels.attention import hip_attention, hip_available
+
+
+@dataclass(frozen=True)
+class AttentionDispatch:
+    requested: str
+    selected: str
+    reason: str
+
+
+def _validate_backend(backend: str) -> None:
+    if backend not in ATTENTION_BACKENDS:
+        raise ValueError(
+            f"attention backend must be one of {ATTENTION_BACKENDS}, got {backend!r}"
+        )
+
+
+def attention_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    valid_token_mask: Optional[torch.Tensor] = None,
+    *,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    backend: str = "auto",
+) -> Tuple[torch.Tensor, AttentionDispatch]:
+    """Execute attention on the HIP kernel and return the output and its record."""
+    _validate_backend(backend)
+    if not hip_available():
+        raise RuntimeError(
+            f"HIP attention was {'forced' if backend == 'hip' else 'requested'} but "
+            "ROCm/the HIP kernel library is unavailable"
+        )
+    support = hip_attention_support(q, k, v, valid_token_mask)
+    if not support.supported:
+        raise ValueError(
+            f"HIP attention was {'forced' if backend == 'hip' else 'requested'} but "
+            f"unsupported: {support.reason}"
+        )
+    output = hip_attention(q, k, v, valid_token_mask, causal=causal, scale=scale)
+    return output, AttentionDispatch(backend, "hip", support.reason)

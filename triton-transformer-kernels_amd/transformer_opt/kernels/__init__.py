@@ -1,0 +1,11 @@
+"""gfx950 HIP kernels behind the reference's kernel-module surface."""
+
+from .attention import hip_attention, hip_available
+from .residual_layer_norm import fused_residual_layer_norm, layer_norm
+
+__all__ = [
+    "fused_residual_layer_norm",
+    "hip_attention",
+    "hip_available",
+    "layer_norm",
+]

@@ -1,0 +1,96 @@
+"""Strict wrapper of the gfx950 HIP fused attention kernel.
+
+Mirrors the reference's ``triton_attention`` (transformer_opt/kernels/
+attention.py:268-360): validate the support contract, allocate the output with
+torch, pick the default scale ``head_dim ** -0.5``, and launch on torch's
+current stream.  Unsupported inputs raise; nothing falls back.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _native
+from ..config import hip_attention_support
+
+_DTYPE_CODE = {
+    torch.float32: _native.TTK_F32,
+    torch.bfloat16: _native.TTK_BF16,
+    torch.float16: _native.TTK_F16,
+}
+
+
+def hip_available() -> bool:
+    """True when a ROCm device is visible and the HIP library loads."""
+    return torch.cuda.is_available() and _native.available()
+
+
+def _vector_ready(t: torch.Tensor) -> bool:
+    """Rows start on 16-byte boundaries (the kernel's 128-bit accesses)."""
+    es = t.element_size()
+    return t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:3])
+
+
+def hip_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    valid_token_mask: Optional[torch.Tensor] = None,
+    *,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Run the HIP fused attention and return the ``[B, S, H, D]`` output.
+
+    Strict low-level wrapper: unsupported inputs raise ``ValueError``, a
+    missing library raises ``RuntimeError``.  Use
+    ``transformer_opt.dispatch.attention_forward`` for the audited entry point.
+    """
+    lib = _native.load()
+    support = hip_attention_support(q, k, v, valid_token_mask)
+    if not support.supported:
+        raise ValueError(f"unsupported HIP attention input: {support.reason}")
+
+    # Arbitrary B/S/H strides are part of the contract; rows that are not
+    # 16-byte aligned are repacked so the kernel keeps its vector loads.
+    if not _vector_ready(q):
+        q = q.contiguous()
+    if not _vector_ready(k):
+        k = k.contiguous()
+    if not _vector_ready(v):
+        v = v.contiguous()
+
+    batch, seq_len, num_heads, head_dim = q.shape
+    if out is None:
+        out = torch.empty((batch, seq_len, num_heads, head_dim), dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or out.stride(-1) != 1 \
+            or not _vector_ready(out):
+        raise ValueError("out must be a [B, S, H, D] tensor like q with 16-byte aligned rows")
+    if batch == 0:
+        return out
+
+    softmax_scale = head_dim ** -0.5 if scale is None else float(scale)
+    mask_ptr = None
+    mask_strides = None
+    if valid_token_mask is not None:
+        mask_ptr = valid_token_mask.data_ptr()
+        mask_strides = _native.strides2(valid_token_mask.stride())
+
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        status = lib.ttk_attention_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), mask_ptr, out.data_ptr(),
+            _DTYPE_CODE[q.dtype],
+            batch, seq_len, num_heads, head_dim,
+            _native.strides3(q.stride()[:3]),
+            _native.strides3(k.stride()[:3]),
+            _native.strides3(v.stride()[:3]),
+            mask_strides,
+            _native.strides3(out.stride()[:3]),
+            softmax_scale, 1 if causal else 0, stream,
+        )
+    _native.check(status, "HIP attention")
+    return out

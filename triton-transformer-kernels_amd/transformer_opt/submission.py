@@ -1,0 +1,335 @@
+"""Encoder model on the gfx950 HIP kernels (the reference's submission surface).
+
+``UserOptimizedTransformer`` keeps the reference's public surface
+(transformer_opt/submission.py:78-723): constructor flags
+``attention_backend`` / ``execution_mode``, the counters
+``attention_backend_counts`` / ``fused_residual_layer_norm_calls`` /
+``cuda_graph_replays``, ``reset_attention_backend_counts()``,
+``clear_cuda_graph()``, ``_can_replay_cuda_graph()``, a state-dict key set
+identical to the organizer baseline, a non-persistent packed-QKV projection
+cache invalidated by parameter versions, and bounded single-graph replay.
+
+What is MI355X-specific:
+
+* every attention runs on the HIP kernel (fp32, bf16, fp16) - the
+  reference's per-shape routing policy between Triton, SDPA and explicit math
+  (submission.py:235-321) is gone, and so is the SDPA counter;
+* every LayerNorm runs on the HIP fused residual + LayerNorm kernel, in the
+  reference's fused order (submission.py:481-525) for all shapes: one
+  standalone norm, then two fused residual+norm calls per layer;
+* the packed QKV projection is used for every width and dtype
+  (submission.py:184-190 restricted it to measured widths);
+* graph replay (torch.cuda.CUDAGraph, i.e. a hipGraph on ROCm) is eligible for
+  every supported shape and dtype instead of an exact measured shape set
+  (submission.py:582-590).
+
+Projections and the FFN stay library GEMMs (hipBLASLt through F.linear).
+The model is forward-inference only: a call with gradients enabled on
+parameters that require them raises, as there is no backward kernel.
+"""
+
+from __future__ import annotations
+
+import threading
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .config import ATTENTION_BACKENDS, SUPPORTED_DTYPES
+from .dispatch import attention_forward
+from .kernels.residual_layer_norm import fused_residual_layer_norm, layer_norm
+from .model import SelfAttention, TransformerBlock, TransformerConfig
+
+__all__ = ["TransformerConfig", "UserOptimizedTransformer"]
+
+_EXECUTION_MODES = ("auto", "eager")
+
+
+class UserOptimizedTransformer(nn.Module):
+    """Pre-LN encoder whose attention and LayerNorms run on gfx950 HIP kernels."""
+
+    def __init__(self, config, attention_backend: str = "auto", execution_mode: str = "auto") -> None:
+        super().__init__()
+        if attention_backend not in ATTENTION_BACKENDS:
+            raise ValueError(
+                f"attention_backend must be one of {ATTENTION_BACKENDS}, got {attention_backend!r}"
+            )
+        if execution_mode not in _EXECUTION_MODES:
+            raise ValueError("execution_mode must be 'auto' or 'eager'")
+        self.config = config
+        self.layers = nn.ModuleList(
+            [TransformerBlock(config.d_model, config.num_heads, config.ffn_dim)
+             for _ in range(config.num_layers)]
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+        self.attention_backend = attention_backend
+        self.execution_mode = execution_mode
+        self._inference_graph = None
+        self._inference_graph_lock = threading.RLock()
+        self.cuda_graph_replays = 0
+        self.attention_backend_counts: Dict[str, int] = {"hip": 0}
+        self.fused_residual_layer_norm_calls = 0
+        # Derived, non-persistent packed projection weights keyed by module id;
+        # kept out of the state dict so its keys equal the baseline's.
+        self._packed_qkv_cache: Dict[int, Tuple[tuple, torch.Tensor, torch.Tensor]] = {}
+
+    # -- counters / pickling -------------------------------------------------
+    def reset_attention_backend_counts(self) -> None:
+        self.attention_backend_counts = {"hip": 0}
+        self.fused_residual_layer_norm_calls = 0
+        self.cuda_graph_replays = 0
+
+    def __getstate__(self):
+        state = super().__getstate__().copy()
+        state["_inference_graph"] = None
+        state.pop("_inference_graph_lock", None)
+        return state
+
+    def __setstate__(self, state):
+        super().__setstate__(state)
+        self._inference_graph_lock = threading.RLock()
+
+    # -- projections -----------------------------------------------------------
+    @staticmethod
+    def _qkv_signature(attn: SelfAttention) -> tuple:
+        tensors = (attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight,
+                   attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias)
+        return tuple((t.data_ptr(), t._version, t.device, t.dtype) for t in tensors if t is not None)
+
+    def _project_qkv(self, attn: SelfAttention, x: torch.Tensor):
+        """One packed GEMM -> strided [B, S, H, D] views of Q, K and V.
+
+        Same cache contract as the reference (submission.py:145-217): the
+        concatenated weight is rebuilt whenever any projection parameter's
+        pointer, version counter, device or dtype changes.
+        """
+        batch, seq_len, _ = x.shape
+        signature = self._qkv_signature(attn)
+        cached = self._packed_qkv_cache.get(id(attn))
+        if cached is None or cached[0] != signature:
+            packed_weight = torch.cat(
+                (attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight), dim=0).detach()
+            packed_bias = torch.cat(
+                (attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias), dim=0).detach()
+            cached = (signature, packed_weight, packed_bias)
+            self._packed_qkv_cache[id(attn)] = cached
+        projected = F.linear(x, cached[1], cached[2])
+        qkv = projected.view(batch, seq_len, 3, attn.num_heads, attn.head_dim)
+        return qkv.unbind(dim=2)
+
+    def _attention(self, attn: SelfAttention, x: torch.Tensor,
+                   valid_token_mask: Optional[torch.Tensor], causal: bool) -> torch.Tensor:
+        batch, seq_len, _ = x.shape
+        q, k, v = self._project_qkv(attn, x)
+        context, dispatch = attention_forward(
+            q, k, v, valid_token_mask, causal=causal, scale=attn.scale,
+            backend=self.attention_backend,
+        )
+        self.attention_backend_counts[dispatch.selected] += 1
+        return attn.out_proj(context.reshape(batch, seq_len, attn.d_model))
+
+    def _fused_residual_norm(self, x, update, norm: nn.LayerNorm, valid_token_mask, *,
+                             zero_invalid_residual=False, zero_invalid_normalized=False):
+        residual, normalized = fused_residual_layer_norm(
+            x, update, norm.weight, norm.bias, norm.eps, valid_token_mask,
+            zero_invalid_residual=zero_invalid_residual,
+            zero_invalid_normalized=zero_invalid_normalized,
+        )
+        self.fused_residual_layer_norm_calls += 1
+        return residual, normalized
+
+    # -- forward -----------------------------------------------------------------
+    def _forward_eager(self, x: torch.Tensor,
+                       valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Fused order of the reference (submission.py:481-525).
+
+        LN(x) once; then per layer: attention, (x, ffn_in) = x + attn,
+        LN2(x + attn); FFN; (x, next_in) = x + ffn, next LN, with invalid rows
+        of x zeroed (the baseline's per-block masked_fill) and invalid rows of
+        the final output zeroed.  Invalid rows never reach a valid row: their
+        keys are masked in every attention and all other ops are row-wise.
+        """
+        if valid_token_mask is not None and not valid_token_mask.is_contiguous():
+            valid_token_mask = valid_token_mask.contiguous()
+        x = x.contiguous()
+        causal = self.config.causal
+        first = self.layers[0].norm1
+        normalized = layer_norm(x, first.weight, first.bias, first.eps)
+        last_index = len(self.layers) - 1
+        for index, layer in enumerate(self.layers):
+            attn_out = self._attention(layer.attention, normalized, valid_token_mask, causal)
+            del normalized
+            x, ffn_input = self._fused_residual_norm(x, attn_out, layer.norm2, valid_token_mask)
+            del attn_out
+            ffn_out = layer.ffn_out(F.gelu(layer.ffn_in(ffn_input), approximate="none"))
+            del ffn_input
+            is_last = index == last_index
+            next_norm = self.final_norm if is_last else self.layers[index + 1].norm1
+            x, normalized = self._fused_residual_norm(
+                x, ffn_out, next_norm, valid_token_mask,
+                zero_invalid_residual=valid_token_mask is not None,
+                zero_invalid_normalized=is_last and valid_token_mask is not None,
+            )
+            del ffn_out
+        return normalized
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self._graph_input_supported(x, valid_token_mask):
+            with self._inference_graph_lock:
+                signature = self._graph_signature(x, valid_token_mask)
+                if signature is not None:
+                    entry = self._inference_graph
+                    if entry is None or entry.signature != signature:
+                        self._inference_graph = None
+                        entry = _InferenceGraph(self, x, valid_token_mask, signature)
+                        self._inference_graph = entry
+                    output = entry.replay(x, valid_token_mask)
+                    for backend, count in entry.backend_counts.items():
+                        self.attention_backend_counts[backend] += count
+                    self.fused_residual_layer_norm_calls += entry.fused_calls
+                    self.cuda_graph_replays += 1
+                    return output
+        return self._forward_eager(x, valid_token_mask)
+
+    # -- graph replay ------------------------------------------------------------
+    def _can_replay_cuda_graph(self, x, valid_token_mask) -> bool:
+        return (self._graph_input_supported(x, valid_token_mask)
+                and self._graph_signature(x, valid_token_mask) is not None)
+
+    def _graph_input_supported(self, x, valid_token_mask) -> bool:
+        """Capture eligibility (reference submission.py:561-601, minus the
+        measured-shape whitelist): eval-mode inference on one ROCm device with a
+        supported dtype, no autograd, no autocast, no hooks, not already
+        capturing."""
+        if (
+            self.execution_mode != "auto"
+            or self.attention_backend != "auto"
+            or not x.is_cuda
+            or x.dtype not in SUPPORTED_DTYPES
+            or x.ndim != 3
+            or not x.is_contiguous()
+            or torch.is_grad_enabled()
+            or self.training
+            or torch.compiler.is_compiling()
+            or torch.cuda.current_device() != x.device.index
+            or torch.cuda.is_current_stream_capturing()
+            or torch.is_autocast_enabled("cuda")
+        ):
+            return False
+        if x.shape[2] != self.config.d_model or x.numel() == 0:
+            return False
+        if valid_token_mask is not None and not (
+            valid_token_mask.shape == x.shape[:2]
+            and valid_token_mask.device == x.device
+            and valid_token_mask.dtype == torch.bool
+            and valid_token_mask.is_contiguous()
+        ):
+            return False
+        if nn.modules.module._global_forward_hooks or nn.modules.module._global_forward_pre_hooks:
+            return False
+        return True
+
+    def _graph_signature(self, x, valid_token_mask):
+        """Everything a captured graph bakes in (reference submission.py:603-641):
+        parameter storage/version/device/dtype, module eps and shapes, hooks,
+        training flags, attention config, input geometry, mask presence and
+        the inference-mode context.  None means "do not capture"."""
+        stack = [self]
+        seen_modules, seen_parameters = set(), set()
+        modules, parameters = [], []
+        while stack:
+            module = stack.pop()
+            identity = id(module)
+            if identity in seen_modules:
+                continue
+            seen_modules.add(identity)
+            if module.training or module._forward_hooks or module._forward_pre_hooks:
+                return None
+            modules.append((identity, getattr(module, "eps", None),
+                            getattr(module, "normalized_shape", None)))
+            for parameter in module._parameters.values():
+                if parameter is None or id(parameter) in seen_parameters:
+                    continue
+                seen_parameters.add(id(parameter))
+                if parameter.is_inference():
+                    return None
+                parameters.append((id(parameter), parameter.data_ptr(), parameter._version,
+                                   parameter.device, parameter.dtype))
+            stack.extend(child for child in reversed(tuple(module._modules.values()))
+                         if child is not None)
+        attention_config = tuple(
+            (layer.attention.d_model, layer.attention.num_heads,
+             layer.attention.head_dim, layer.attention.scale)
+            for layer in self.layers
+        )
+        return (
+            tuple(parameters), tuple(modules), attention_config, self.config, self.attention_backend,
+            x.device, tuple(x.shape), x.dtype, valid_token_mask is not None,
+            torch.backends.cuda.matmul.allow_tf32, torch.is_inference_mode_enabled(),
+        )
+
+    def clear_cuda_graph(self) -> None:
+        """Release the single cached capture; a later eligible call rebuilds it."""
+        with self._inference_graph_lock:
+            self._inference_graph = None
+
+    def _apply(self, fn, recurse=True):
+        # Device/dtype moves must not keep the old graph pool or packed weights.
+        self.clear_cuda_graph()
+        self._packed_qkv_cache.clear()
+        return super()._apply(fn, recurse=recurse)
+
+
+class _InferenceGraph:
+    """One captured forward with static input buffers (reference submission.py:
+    674-723): warm up on a side stream, capture ``_forward_eager``, record the
+    backend counts the capture performed, and on replay copy fresh inputs in,
+    replay, and return a clone so earlier results are never overwritten."""
+
+    def __init__(self, model: UserOptimizedTransformer, x, mask, signature):
+        self.signature = signature
+        self.x = x.clone()
+        self.mask = mask.clone() if mask is not None else None
+        # Keep captured parameter storage alive across state/device changes.
+        self.parameters = tuple(parameter.detach() for parameter in model.parameters())
+        before = dict(model.attention_backend_counts)
+        fused_before = model.fused_residual_layer_norm_calls
+        stream = torch.cuda.Stream(device=x.device)
+        current = torch.cuda.current_stream(x.device)
+        stream.wait_stream(current)
+        try:
+            with torch.cuda.stream(stream):
+                for _ in range(3):
+                    model._forward_eager(self.x, self.mask)
+            current.wait_stream(stream)
+            capture_before = dict(model.attention_backend_counts)
+            capture_fused_before = model.fused_residual_layer_norm_calls
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=stream):
+                self.output = model._forward_eager(self.x, self.mask)
+            current.wait_stream(stream)
+            self.backend_counts = {
+                backend: count - capture_before.get(backend, 0)
+                for backend, count in model.attention_backend_counts.items()
+            }
+            self.fused_calls = model.fused_residual_layer_norm_calls - capture_fused_before
+            self.packed = tuple(model._packed_qkv_cache.values())
+            self.complete = torch.cuda.Event()
+            self.complete.record(current)
+        finally:
+            # Warm-up and capture are set-up, not user-visible forwards.
+            model.attention_backend_counts = before
+            model.fused_residual_layer_norm_calls = fused_before
+
+    def replay(self, x, mask):
+        current = torch.cuda.current_stream(x.device)
+        current.wait_event(self.complete)
+        self.x.copy_(x)
+        if self.mask is not None:
+            self.mask.copy_(mask)
+        self.graph.replay()
+        output = self.output.clone()
+        self.complete.record(current)
+        return output
