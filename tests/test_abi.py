@@ -1,0 +1,127 @@
+"""The C ABI library: it loads, exports every declared symbol, and rejects bad
+arguments before touching the device (so these run without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import sys
+import threading
+from pathlib import Path
+
+import pytest
+
+from transformer_opt import _native
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "ttk_hip.h"
+
+
+def declared_functions() -> list:
+    text = HEADER.read_text()
+    return re.findall(r"^\s*(?:const\s+)?[a-z_]+\*?\s+\*?(ttk_[a-z0-9_]+)\s*\(", text, re.MULTILINE)
+
+
+def test_header_declares_the_exported_symbols():
+    assert set(declared_functions()) == set(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_native.library_path())],
+                        capture_output=True, text=True, check=True).stdout
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}$", nm, re.MULTILINE), name
+
+
+def test_abi_version_matches_header():
+    version = int(re.search(r"#define TTK_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert _native.load().ttk_abi_version() == version == _native.ABI_VERSION
+
+
+def _attention(lib, **over):
+    s3 = (ctypes.c_int64 * 3)(16 * 64, 64, 64 * 0 + 64)
+    args = dict(q=16, k=32, v=48, mask=None, out=64, dtype=0, B=1, S=16, H=1, D=64,
+                qs=s3, ks=s3, vs=s3, ms=None, os=s3, scale=0.125, causal=0, stream=None)
+    args.update(over)
+    return lib.ttk_attention_fwd(args["q"], args["k"], args["v"], args["mask"], args["out"], args["dtype"],
+                                 args["B"], args["S"], args["H"], args["D"], args["qs"], args["ks"],
+                                 args["vs"], args["ms"], args["os"], args["scale"], args["causal"],
+                                 args["stream"])
+
+
+def test_attention_argument_errors_are_reported_without_launching():
+    lib = _native.load()
+    assert _attention(lib, D=48) == _native.TTK_EUNSUPPORTED
+    assert "head_dim=48" in _native.last_error()
+    assert _attention(lib, S=0) == _native.TTK_EINVAL
+    assert "must be positive" in _native.last_error()
+    assert _attention(lib, dtype=7) == _native.TTK_EUNSUPPORTED
+    assert _attention(lib, qs=None) == _native.TTK_EINVAL
+    assert _attention(lib, q=None) == _native.TTK_EINVAL
+    assert _attention(lib, q=17) == _native.TTK_EUNSUPPORTED
+    assert "16-byte aligned" in _native.last_error()
+    bad = (ctypes.c_int64 * 3)(16 * 64, 63, 64)
+    assert _attention(lib, ks=bad) == _native.TTK_EUNSUPPORTED
+    assert "stride" in _native.last_error()
+    assert _attention(lib, mask=16, ms=None) == _native.TTK_EINVAL
+    # An empty batch is a valid no-op (nothing is launched).
+    assert _attention(lib, B=0) == _native.TTK_OK
+    assert _native.last_error() == ""
+
+
+def test_layernorm_argument_errors_are_reported_without_launching():
+    lib = _native.load()
+    f = lib.ttk_residual_layernorm_fwd
+    assert f(16, 16, 16, None, None, 16, 16, 0, 4, 0, 1e-5, 0, 0, None) == _native.TTK_EINVAL
+    assert f(16, 16, 16, None, None, 16, 16, 0, 4, 70000, 1e-5, 0, 0, None) == _native.TTK_EUNSUPPORTED
+    assert "65536" in _native.last_error()
+    assert f(16, 16, 16, None, None, 16, 16, 0, 4, 128, 1e-5, 1, 0, None) == _native.TTK_EINVAL
+    assert "requires valid_token_mask" in _native.last_error()
+    assert f(None, 16, 16, None, None, 16, 16, 0, 4, 128, 1e-5, 0, 0, None) == _native.TTK_EINVAL
+    assert f(16, 16, 16, None, None, 16, 16, 9, 4, 128, 1e-5, 0, 0, None) == _native.TTK_EUNSUPPORTED
+    assert f(16, 16, 16, None, None, 16, 16, 0, 0, 128, 1e-5, 0, 0, None) == _native.TTK_OK
+
+
+def test_last_error_is_thread_local():
+    lib = _native.load()
+    assert _attention(lib, D=48) == _native.TTK_EUNSUPPORTED
+    seen = {}
+
+    def other():
+        seen["msg"] = _native.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "head_dim" in _native.last_error()
+
+
+def test_check_maps_status_to_reference_exception_types():
+    lib = _native.load()
+    _attention(lib, D=48)
+    with pytest.raises(ValueError, match="head_dim"):
+        _native.check(_native.TTK_EUNSUPPORTED, "HIP attention")
+    with pytest.raises(RuntimeError):
+        _native.check(_native.TTK_ELAUNCH, "HIP attention")
+    _native.check(_native.TTK_OK, "noop")
+
+
+def test_missing_library_fails_loudly_in_a_fresh_process(tmp_path):
+    code = (
+        "import sys; sys.path.insert(0, %r); sys.path.insert(0, %r)\n"
+        "import torch\n"
+        "from transformer_opt import _native, attention_forward\n"
+        "try:\n    _native.load()\nexcept RuntimeError as e:\n    print('LOAD', 'not found' in str(e))\n"
+        "q = torch.zeros(1, 4, 1, 8)\n"
+        "try:\n    attention_forward(q, q, q, backend='hip')\nexcept RuntimeError as e:\n    print('FWD', 'unavailable' in str(e))\n"
+    ) % (str(REPO), str(REPO / "triton-transformer-kernels_amd"))
+    env = {"TTK_HIP_LIBRARY": str(tmp_path / "missing.so"), "PATH": "/usr/bin:/bin",
+           "HIP_VISIBLE_DEVICES": "", "CUDA_VISIBLE_DEVICES": ""}
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert "LOAD True" in out.stdout, out.stderr
+    assert "FWD True" in out.stdout, out.stderr

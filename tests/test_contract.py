@@ -1,0 +1,151 @@
+"""Host-side contract of the product surface (reference tests/test_dispatch.py,
+tests/test_correctness.py and tests/test_cuda_graph_inference.py, CPU parts).
+
+No kernel runs here: every call either validates and raises, or inspects
+metadata.  Where the reference fell back to SDPA or explicit math on CPU, the
+HIP build raises instead (there is no fallback in the product path).
+"""
+
+from __future__ import annotations
+
+import copy
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+from transformer_opt import ATTENTION_BACKENDS, attention_forward, hip_attention_support
+from transformer_opt.config import attention_launch_config, triton_attention_support
+from transformer_opt.kernels import fused_residual_layer_norm, layer_norm
+from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
+
+REPO = Path(__file__).resolve().parent.parent
+
+
+def _cpu_qkv(dtype=torch.float32):
+    q = torch.randn(1, 8, 2, 16, dtype=dtype)
+    return q, torch.randn_like(q), torch.randn_like(q)
+
+
+def test_backends_are_auto_and_hip_only():
+    assert ATTENTION_BACKENDS == ("auto", "hip")
+    assert triton_attention_support is hip_attention_support
+
+
+def test_invalid_backend_is_rejected():
+    q, k, v = _cpu_qkv()
+    with pytest.raises(ValueError, match="attention backend"):
+        attention_forward(q, k, v, backend="mystery")
+    with pytest.raises(ValueError, match="attention backend"):
+        attention_forward(q, k, v, backend="sdpa")
+
+
+def test_cpu_tensors_fail_loudly_instead_of_falling_back():
+    q, k, v = _cpu_qkv()
+    for backend in ("auto", "hip"):
+        with pytest.raises((RuntimeError, ValueError), match="HIP attention was"):
+            attention_forward(q, k, v, backend=backend)
+
+
+@pytest.mark.parametrize("bad,reason", [
+    (lambda q: (q, q, q, torch.ones(1, 7, dtype=torch.bool)), "shape [batch, sequence]"),
+    (lambda q: (q[0], q[0], q[0], None), "shape [batch, sequence, heads, head_dim]"),
+    (lambda q: (q, q[:, :4], q, None), "identical shapes"),
+    (lambda q: (q, q.double(), q, None), "identical dtypes"),
+    (lambda q: (q.transpose(2, 3).contiguous().transpose(2, 3), q, q, None), "head-dimension stride"),
+    (lambda q: (q, q, q, torch.ones(1, 8)), "dtype torch.bool"),
+    (lambda q: (q, q, q, None), "ROCm device"),
+])
+def test_support_check_explains_refusals(bad, reason):
+    q = torch.randn(1, 8, 2, 16)
+    result = hip_attention_support(*bad(q))
+    assert not result.supported
+    assert reason in result.reason
+
+
+def test_launch_config_is_the_fixed_gfx950_tile():
+    assert attention_launch_config(64, torch.float32) == attention_launch_config(64)
+    fp32_64 = attention_launch_config(64, torch.float32)
+    assert (fp32_64.block_m, fp32_64.block_n, fp32_64.num_waves, fp32_64.lds_stages) == (128, 64, 4, 2)
+    assert attention_launch_config(128, torch.float32).block_n == 32
+    assert attention_launch_config(128, torch.bfloat16).block_n == 64
+    assert attention_launch_config(8, torch.float16).block_m == 128
+    with pytest.raises(ValueError, match="head_dim=48"):
+        attention_launch_config(48)
+
+
+def test_fused_layer_norm_contract_errors():
+    x = torch.randn(2, 5, 16)
+    w = torch.ones(16)
+    with pytest.raises(ValueError, match="ROCm device"):
+        fused_residual_layer_norm(x, x, w, None, 1e-5)
+    with pytest.raises(ValueError, match="same rank-two-or-higher shape"):
+        fused_residual_layer_norm(x, x[:, :4], w, None, 1e-5)
+    with pytest.raises(ValueError, match="same rank-two-or-higher shape"):
+        fused_residual_layer_norm(x[0, 0], x[0, 0], w, None, 1e-5)
+    with pytest.raises(ValueError):
+        layer_norm(x, w, None, 1e-5)
+
+
+def test_zeroing_without_mask_is_rejected_before_device_checks():
+    # The reference raises this ValueError too (residual_layer_norm.py:200-201).
+    x = torch.randn(2, 5, 16)
+    if torch.cuda.is_available():
+        x = x.cuda()
+    w = torch.ones(16, device=x.device)
+    if x.is_cuda:
+        with pytest.raises(ValueError, match="requires valid_token_mask"):
+            fused_residual_layer_norm(x, x, w, None, 1e-5, zero_invalid_residual=True)
+
+
+def test_model_constructor_validation_and_state_surface():
+    cfg = TransformerConfig(1, 128, 128, 4, 128, 4, True)
+    with pytest.raises(ValueError, match="execution_mode"):
+        UserOptimizedTransformer(cfg, execution_mode="invalid")
+    with pytest.raises(ValueError, match="attention_backend"):
+        UserOptimizedTransformer(cfg, attention_backend="triton")
+    model = UserOptimizedTransformer(cfg).eval()
+    assert model.attention_backend_counts == {"hip": 0}
+    assert model.fused_residual_layer_norm_calls == 0 and model.cuda_graph_replays == 0
+    cloned = copy.deepcopy(model)
+    assert cloned.state_dict().keys() == model.state_dict().keys()
+    assert cloned._inference_graph is None
+    with torch.inference_mode():
+        assert not model._can_replay_cuda_graph(torch.randn(1, 128, 128), None)
+    keys = set(model.state_dict().keys())
+    assert "layers.0.attention.q_proj.weight" in keys and "final_norm.bias" in keys
+    assert not any("packed" in key for key in keys)
+
+
+def test_model_forward_on_cpu_fails_loudly():
+    cfg = TransformerConfig(1, 16, 32, 2, 64, 1, False)
+    model = UserOptimizedTransformer(cfg).eval()
+    with torch.inference_mode(), pytest.raises((RuntimeError, ValueError)):
+        model(torch.randn(1, 16, 32))
+
+
+def test_config_validation():
+    TransformerConfig(1, 1, 8, 2, 8, 1, False).validate()
+    with pytest.raises(ValueError, match="divisible"):
+        TransformerConfig(1, 1, 10, 3, 8, 1, False).validate()
+    with pytest.raises(ValueError, match="positive"):
+        TransformerConfig(0, 1, 8, 2, 8, 1, False).validate()
+
+
+def test_product_never_imports_the_oracle():
+    pkg = REPO / "triton-transformer-kernels_amd"
+    for path in pkg.rglob("*.py"):
+        text = path.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, path
+    for path in (pkg / "csrc").glob("*"):
+        assert "oracle" not in path.read_text(), path
+
+
+def test_bench_rejects_multi_gpu_requests():
+    import subprocess
+
+    out = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "8"],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 2
+    assert "one MI355X" in out.stderr

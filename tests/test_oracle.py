@@ -1,0 +1,313 @@
+"""Pins of the CPU oracle (runs without a GPU).
+
+The reference holds no golden vectors for this path, so the oracle is pinned
+by (a) the float64 fixtures in tests/golden/ (written by make_golden.py from
+its own vectorised float64 code), (b) the independent loop brute force,
+(c) library routines (F.scaled_dot_product_attention, F.layer_norm,
+nn.TransformerEncoderLayer), (d) closed forms and invariants.  Each planted
+mistake at the end (a dropped scale, an off-by-one causal mask, a transposed
+operand, an ignored key mask, an unbiased variance, a missing residual) must be
+caught by at least one of these pins.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle.attention import (
+    brute_force_attention_f64,
+    chunked_kernel_contract_attention,
+    explicit_attention,
+    kernel_contract_attention,
+)
+from oracle.layernorm import brute_force_layer_norm_f64, explicit_residual_layer_norm
+from oracle.model import (
+    BaselineTransformer,
+    TransformerConfig,
+    compare_outputs,
+    copy_model_weights,
+    generate_random_case,
+)
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "golden_v1.npz"
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def attention_cases(golden):
+    names = sorted({key.split("/")[1] for key in golden.files if key.startswith("attn/")})
+    for name in names:
+        q, k, v = (torch.from_numpy(golden[f"attn/{name}/{t}"]) for t in "qkv")
+        mask = golden[f"attn/{name}/mask"]
+        mask = torch.from_numpy(mask) if mask.size else None
+        causal, scale, _ = golden[f"attn/{name}/meta"]
+        yield name, q, k, v, mask, bool(causal), float(scale), golden[f"attn/{name}/expected"]
+
+
+def ln_cases(golden):
+    names = sorted({key.split("/")[1] for key in golden.files if key.startswith("ln/")})
+    for name in names:
+        get = lambda t: golden[f"ln/{name}/{t}"]  # noqa: E731
+        b = get("b")
+        mask = get("mask")
+        eps, zr, zn = get("meta")
+        yield (name, torch.from_numpy(get("x")), torch.from_numpy(get("u")), torch.from_numpy(get("w")),
+               torch.from_numpy(b) if b.size else None, torch.from_numpy(mask) if mask.size else None,
+               float(eps), bool(zr), bool(zn), get("residual"), get("normalized"))
+
+
+# ---------------------------------------------------------------- attention --
+def test_oracle_attention_matches_golden_fixtures(golden):
+    seen = 0
+    for name, q, k, v, mask, causal, scale, expected in attention_cases(golden):
+        out = kernel_contract_attention(q, k, v, mask, causal, scale).double().numpy()
+        assert np.abs(out - expected).max() < 1e-5, name
+        seen += 1
+    assert seen >= 8
+
+
+def test_brute_force_matches_golden_fixtures(golden):
+    for name, q, k, v, mask, causal, scale, expected in attention_cases(golden):
+        bf = brute_force_attention_f64(q.numpy(), k.numpy(), v.numpy(),
+                                       None if mask is None else mask.numpy(), causal, scale)
+        assert np.abs(bf - expected).max() < 1e-10, name
+
+
+def test_all_masked_fixture_is_zero_in_contract_and_nan_in_explicit(golden):
+    q, k, v = (torch.from_numpy(golden[f"attn/all_masked_d8/{t}"]) for t in "qkv")
+    mask = torch.from_numpy(golden["attn/all_masked_d8/mask"])
+    assert torch.count_nonzero(kernel_contract_attention(q, k, v, mask, True)) == 0
+    # The reference's explicit math yields NaN there (softmax of all -inf).
+    assert torch.isnan(explicit_attention(q, k, v, mask, True)).all()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_oracle_matches_sdpa(causal, with_mask):
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(2, 45, 3, 32, generator=g) for _ in range(3))
+    mask = (torch.arange(45)[None, :] < torch.tensor([[45], [30]])) if with_mask else None
+    ours = explicit_attention(q, k, v, mask, causal)
+    attn_mask = None
+    if with_mask or causal:
+        allowed = torch.ones(2, 1, 45, 45, dtype=torch.bool)
+        if causal:
+            allowed &= torch.ones(45, 45, dtype=torch.bool).tril()
+        if with_mask:
+            allowed &= mask[:, None, None, :]
+        attn_mask = allowed
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                         attn_mask=attn_mask).transpose(1, 2)
+    assert (ours - ref).abs().max() < 1e-5
+
+
+def test_chunked_oracle_equals_full_oracle():
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(2, 70, 3, 16, generator=g) for _ in range(3))
+    mask = torch.arange(70)[None, :] < torch.tensor([[70], [1]])
+    for causal in (False, True):
+        full = kernel_contract_attention(q, k, v, mask, causal)
+        heads = [(0, 1), (1, 2), (1, 0)]
+        chunked = chunked_kernel_contract_attention(q, k, v, mask, causal, heads=heads)
+        expected = torch.stack([full[b, :, h, :] for b, h in heads])
+        assert (chunked - expected).abs().max() < 1e-6
+        rows = chunked_kernel_contract_attention(q, k, v, mask, causal, heads=[(1, 2)],
+                                                 query_rows=slice(10, 40))
+        assert (rows[0] - full[1, 10:40, 2, :]).abs().max() < 1e-6
+
+
+def test_attention_closed_forms():
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, 33, 2, 16, generator=g)
+    k = torch.randn(1, 1, 2, 16, generator=g).expand(1, 33, 2, 16).contiguous()
+    v = torch.randn(1, 33, 2, 16, generator=g)
+    out = kernel_contract_attention(q, k, v, None, True)
+    cumulative_mean = torch.cumsum(v, dim=1) / torch.arange(1, 34)[None, :, None, None]
+    assert (out - cumulative_mean).abs().max() < 1e-5
+    assert torch.allclose(out[:, 0], v[:, 0])
+    # Permuting keys and values together leaves non-causal attention unchanged.
+    k2 = torch.randn(1, 33, 2, 16, generator=g)
+    perm = torch.randperm(33, generator=g)
+    a = kernel_contract_attention(q, k2, v, None, False)
+    b = kernel_contract_attention(q, k2[:, perm], v[:, perm], None, False)
+    assert (a - b).abs().max() < 1e-5
+
+
+# ---------------------------------------------------------------- layernorm --
+def test_layer_norm_oracle_matches_golden_fixtures(golden):
+    for name, x, u, w, b, mask, eps, zr, zn, residual, normalized in ln_cases(golden):
+        r, y = explicit_residual_layer_norm(x, u, w, b, eps, mask,
+                                            zero_invalid_residual=zr, zero_invalid_normalized=zn)
+        assert np.array_equal(r.numpy(), residual), name
+        assert np.abs(y.double().numpy() - normalized).max() < 2e-5, name
+        bf = brute_force_layer_norm_f64(r.numpy(), w.numpy(), None if b is None else b.numpy(), eps)
+        if zn:
+            bf = np.where(mask.numpy()[:, None], bf, 0.0)
+        assert np.abs(bf - normalized).max() < 1e-12, name
+
+
+def test_layer_norm_closed_forms():
+    hidden = 64
+    w = torch.linspace(0.5, 1.5, hidden)
+    b = torch.linspace(-1, 1, hidden)
+    x = torch.full((1, hidden), 2.5)
+    _, y = explicit_residual_layer_norm(x, torch.zeros_like(x), w, b, 1e-5)
+    assert torch.allclose(y[0], b)
+    a = 0.5
+    x = torch.where(torch.arange(hidden) % 2 == 0, a, -a)[None, :]
+    _, y = explicit_residual_layer_norm(x, torch.zeros_like(x), w, b, 1e-5)
+    sign = torch.where(torch.arange(hidden) % 2 == 0, 1.0, -1.0)
+    assert (y[0] - (sign * a / (a * a + 1e-5) ** 0.5 * w + b)).abs().max() < 1e-6
+
+
+# -------------------------------------------------------------------- model --
+def _encoder_reference(baseline: BaselineTransformer, x, causal):
+    """The same stack through nn.TransformerEncoderLayer(norm_first=True)."""
+    cfg = baseline.config
+    y = x
+    mask = torch.ones(cfg.seq_len, cfg.seq_len, dtype=torch.bool).triu(1) if causal else None
+    for block in baseline.layers:
+        layer = nn.TransformerEncoderLayer(cfg.d_model, cfg.num_heads, cfg.ffn_dim, dropout=0.0,
+                                           activation="gelu", batch_first=True, norm_first=True)
+        a = block.attention
+        with torch.no_grad():
+            layer.self_attn.in_proj_weight.copy_(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]))
+            layer.self_attn.in_proj_bias.copy_(torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]))
+            layer.self_attn.out_proj.weight.copy_(a.out_proj.weight)
+            layer.self_attn.out_proj.bias.copy_(a.out_proj.bias)
+            layer.linear1.weight.copy_(block.ffn_in.weight)
+            layer.linear1.bias.copy_(block.ffn_in.bias)
+            layer.linear2.weight.copy_(block.ffn_out.weight)
+            layer.linear2.bias.copy_(block.ffn_out.bias)
+            layer.norm1.load_state_dict(block.norm1.state_dict())
+            layer.norm2.load_state_dict(block.norm2.state_dict())
+        layer.eval()
+        y = layer(y, src_mask=mask)
+    return baseline.final_norm(y)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_model_oracle_matches_torch_transformer_encoder(causal):
+    torch.manual_seed(0)
+    cfg = TransformerConfig(2, 24, 64, 4, 128, 2, causal)
+    baseline = BaselineTransformer(cfg).eval()
+    x = torch.randn(2, 24, 64)
+    with torch.no_grad():
+        ours = baseline(x)
+        ref = _encoder_reference(baseline, x, causal)
+    assert (ours - ref).abs().max() < 1e-5
+
+
+def test_model_oracle_padding_rows_zero_and_valid_rows_unaffected():
+    torch.manual_seed(1)
+    cfg = TransformerConfig(2, 20, 32, 2, 64, 2, False)
+    baseline = BaselineTransformer(cfg).eval()
+    x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 9, 0.4, 1.0)
+    assert mask is not None and not bool(mask.all())
+    with torch.no_grad():
+        out = baseline(x, mask)
+        # Valid rows equal a run on the valid prefix alone (keys beyond are masked).
+        for b in range(2):
+            n = int(mask[b].sum())
+            single_cfg = TransformerConfig(1, n, 32, 2, 64, 2, False)
+            single = BaselineTransformer(single_cfg).eval()
+            single.load_state_dict(baseline.state_dict())
+            alone = single(x[b:b + 1, :n])
+            assert (out[b, :n] - alone[0]).abs().max() < 1e-5
+    assert torch.count_nonzero(out[~mask]) == 0
+
+
+def test_compare_outputs_is_the_or_rule_not_isclose():
+    ref = torch.tensor([1.0, 0.0, 100.0, 1.0])
+    opt = torch.tensor([1.0105, 0.0009, 100.9, float("nan")])
+    res = compare_outputs(ref, opt, rtol=0.01, atol=0.001)
+    # 1.0105: |d|=0.0105 > atol and > 1%: fails although isclose would pass it.
+    assert res.failed_elements == 2
+    assert torch.isclose(torch.tensor(1.0105), torch.tensor(1.0), rtol=0.01, atol=0.001)
+
+
+def test_generate_random_case_contract():
+    cfg = TransformerConfig(3, 16, 8, 2, 16, 1, False)
+    x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 5, 0.0, 2.0)
+    assert mask is None and x.shape == (3, 16, 8)
+    x2, _ = generate_random_case(cfg, torch.device("cpu"), torch.float32, 5, 0.0, 2.0)
+    assert torch.equal(x, x2)
+    x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 5, 0.5, 1.0)
+    lengths = mask.sum(1)
+    assert bool((lengths >= 8).all()) and bool((lengths <= 16).all())
+    assert torch.count_nonzero(x[~mask]) == 0
+
+
+def test_strict_weight_copy_between_oracle_and_product_module_tree():
+    import transformer_opt.model  # noqa: F401  (module tree only; no kernels run)
+    from transformer_opt.submission import UserOptimizedTransformer
+
+    cfg = TransformerConfig(2, 16, 64, 8, 128, 2, False)
+    baseline = BaselineTransformer(cfg)
+    product = UserOptimizedTransformer(cfg)
+    assert baseline.state_dict().keys() == product.state_dict().keys()
+    copy_model_weights(baseline, product, strict=True)
+    copy_model_weights(product, baseline, strict=True)
+
+
+# ------------------------------------------------------------ planted mistakes --
+def _golden_attention_error(golden, fn):
+    worst = 0.0
+    for _, q, k, v, mask, causal, scale, expected in attention_cases(golden):
+        out = fn(q, k, v, mask, causal, scale).double().numpy()
+        out = np.nan_to_num(out, nan=1e9)
+        worst = max(worst, float(np.abs(out - expected).max()))
+    return worst
+
+
+def _mistake_no_scale(q, k, v, mask, causal, scale):
+    return kernel_contract_attention(q, k, v, mask, causal, 1.0)
+
+
+def _mistake_causal_off_by_one(q, k, v, mask, causal, scale):
+    if not causal:
+        return kernel_contract_attention(q, k, v, mask, causal, scale)
+    s = q.shape[1]
+    allowed = torch.ones(s, s, dtype=torch.bool).tril(-1)  # excludes the diagonal
+    if mask is not None:
+        allowed = allowed[None] & mask[:, None, :]
+        allowed = allowed[:, None]
+    scores = torch.matmul(q.transpose(1, 2), k.transpose(1, 2).transpose(-1, -2)) * scale
+    scores = scores.masked_fill(~allowed, float("-inf"))
+    p = torch.softmax(scores, -1).nan_to_num(0.0)
+    return torch.matmul(p, v.transpose(1, 2)).transpose(1, 2)
+
+
+def _mistake_transposed_value(q, k, v, mask, causal, scale):
+    return kernel_contract_attention(q, k, v.flip(1), mask, causal, scale)
+
+
+def _mistake_ignored_mask(q, k, v, mask, causal, scale):
+    return kernel_contract_attention(q, k, v, None, causal, scale)
+
+
+@pytest.mark.parametrize("mistake", [_mistake_no_scale, _mistake_causal_off_by_one,
+                                     _mistake_transposed_value, _mistake_ignored_mask])
+def test_planted_attention_mistakes_are_caught_by_golden(golden, mistake):
+    assert _golden_attention_error(golden, mistake) > 1e-2
+
+
+def test_planted_layer_norm_mistakes_are_caught(golden):
+    for name, x, u, w, b, mask, eps, zr, zn, residual, normalized in ln_cases(golden):
+        r = torch.from_numpy(residual)
+        unbiased = (r - r.mean(-1, keepdim=True)) / torch.sqrt(r.var(-1, keepdim=True, unbiased=True) + eps)
+        unbiased = unbiased * w + (b if b is not None else 0)
+        if zn:
+            unbiased = unbiased.masked_fill(~mask[:, None], 0)
+        assert np.abs(unbiased.double().numpy() - normalized).max() > 1e-4, name
+        no_residual = F.layer_norm(x, (x.shape[-1],), w, b, eps)
+        assert np.abs(no_residual.double().numpy() - normalized).max() > 1e-2, name

@@ -220,6 +220,8 @@ class UserOptimizedTransformer(nn.Module):
             return False
         if x.shape[2] != self.config.d_model or x.numel() == 0:
             return False
+        if x.dtype != self.final_norm.weight.dtype or x.device != self.final_norm.weight.device:
+            return False
         if valid_token_mask is not None and not (
             valid_token_mask.shape == x.shape[:2]
             and valid_token_mask.device == x.device
