@@ -10,8 +10,9 @@ whole-job throughput in TFLOP/s of algorithmic causal FLOPs
 clock of exactly K steps bracketed by device synchronisation.
 
 Also reported in the same line:
-* ``roofline``: the attention kernel's achieved TFLOP/s from per-launch HIP
-  events on the launch stream, against the 157.3 TFLOP/s fp32 MFMA peak;
+* ``roofline``: the attention kernel's achieved TFLOP/s from HIP events on
+  the launch stream around the K back-to-back launches (elapsed / K = the
+  average launch duration), against the 157.3 TFLOP/s fp32 MFMA peak;
   ``traffic`` (HBM bytes per launch) comes from the committed rocprofv3 PMC
   summary in profiles/traffic.json when present, else null;
 * ``cpu_baseline``: the reference's explicit PyTorch attention (the oracle's
@@ -198,6 +199,60 @@ def cpu_baseline(time_budget_s: float = 20.0):
     }
 
 
+def profile_only(which: str, steps: int, warmup: int) -> int:
+    """Launch one kernel `steps` times (after `warmup`) for a profiler run.
+
+    attention:      fp32 causal [8,1024,16,64] (the headline step)
+    attention_bf16: bf16 causal [1,16384,32,128] (config 5a)
+    layernorm:      fp32 residual+LN rows=32768 hidden=4096 (config 3), one input set
+    copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
+                    FETCH_SIZE and WRITE_SIZE should each read 262144 KiB per dispatch)
+    """
+    import torch
+
+    from transformer_opt.kernels import fused_residual_layer_norm, hip_attention
+
+    if which == "attention":
+        q, k, v = make_qkv(8, 1024, 16, 64, torch.float32, seed=1234)
+        out = torch.empty_like(q)
+        fn = lambda: hip_attention(q, k, v, causal=True, out=out)  # noqa: E731
+        work = attention_flops(8, 16, 1024, 64, True)
+    elif which == "attention_bf16":
+        q, k, v = make_qkv(1, 16384, 32, 128, torch.bfloat16, seed=5)
+        out = torch.empty_like(q)
+        fn = lambda: hip_attention(q, k, v, causal=True, out=out)  # noqa: E731
+        work = attention_flops(1, 32, 16384, 128, True)
+    elif which == "layernorm":
+        x = torch.randn(32768, 4096, device="cuda")
+        u = torch.randn_like(x)
+        w = torch.rand(4096, device="cuda") + 0.5
+        b = torch.randn(4096, device="cuda") * 0.1
+        fn = lambda: fused_residual_layer_norm(x, u, w, b, 1e-5)  # noqa: E731
+        work = layer_norm_bytes(32768, 4096)
+    else:
+        src = torch.empty(64 * 1024 * 1024, device="cuda")
+        dst = torch.empty_like(src)
+        fn = lambda: dst.copy_(src)  # noqa: E731
+        work = 2.0 * src.numel() * 4
+    with torch.inference_mode():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        begin = torch.cuda.Event(enable_timing=True)
+        finish = torch.cuda.Event(enable_timing=True)
+        begin.record()
+        for _ in range(steps):
+            fn()
+        finish.record()
+        torch.cuda.synchronize()
+    ms = begin.elapsed_time(finish) / steps
+    rate = work / (ms * 1e-3) / (1e9 if which in ("layernorm", "copy") else 1e12)
+    unit = "GB/s" if which in ("layernorm", "copy") else "TFLOP/s"
+    print(json.dumps({"profile_only": which, "steps": steps, "avg_launch_us": round(ms * 1e3, 2),
+                      "rate": round(rate, 2), "unit": unit}), flush=True)
+    return 0
+
+
 def load_traffic(key: str):
     path = REPO / "profiles" / "traffic.json"
     if not path.exists():
@@ -215,6 +270,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16"),
+                        help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -235,6 +292,8 @@ def main() -> int:
     _native.load()
     dev_name = torch.cuda.get_device_name(0)
     log(f"device {dev_name}; library {_native.library_path()}")
+    if args.profile_only:
+        return profile_only(args.profile_only, args.steps, args.warmup)
 
     # ---- headline: config 2, fp32 causal attention, S=1024 -----------------
     B, S, H, D = 8, 1024, 16, 64
@@ -246,22 +305,23 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
+    # The kernel is launched on torch's current stream, so events recorded on
+    # that stream bracket exactly the K back-to-back launches: their elapsed
+    # time / K is the average launch duration (what rocprofv3 --stats reports).
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    begin = torch.cuda.Event(enable_timing=True)
+    finish = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
+    begin.record(stream)
+    for _ in range(args.steps):
         step()
-        ends[i].record(stream)
+    finish.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     flops = attention_flops(B, H, S, D, True)
     value = flops * args.steps / wall / 1e12
-    avg_launch_ms = sum(launch_ms) / len(launch_ms)
+    avg_launch_ms = begin.elapsed_time(finish) / args.steps
     achieved = flops / (avg_launch_ms * 1e-3) / 1e12
     log(f"attention fp32 causal [8,1024,16,64]: {value:.2f} TFLOP/s wall, "
         f"{achieved:.2f} TFLOP/s per launch ({avg_launch_ms * 1e3:.1f} us)")

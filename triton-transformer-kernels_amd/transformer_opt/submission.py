@@ -291,6 +291,16 @@ class _InferenceGraph:
     replay, and return a clone so earlier results are never overwritten."""
 
     def __init__(self, model: UserOptimizedTransformer, x, mask, signature):
+        # Warm-up and capture run with inference mode off.  torch allocates the
+        # generator's graph-safe RNG state tensors at the first capture and
+        # updates them in place at every later one; allocated inside inference
+        # mode they would become inference tensors and a later capture outside
+        # it would fail.  Replay clones the output in the caller's context, so
+        # returned tensors still follow the caller's mode.
+        with torch.inference_mode(False), torch.no_grad():
+            self._capture(model, x, mask, signature)
+
+    def _capture(self, model: UserOptimizedTransformer, x, mask, signature):
         self.signature = signature
         self.x = x.clone()
         self.mask = mask.clone() if mask is not None else None
