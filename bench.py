@@ -199,10 +199,10 @@ def cpu_baseline(time_budget_s: float = 20.0):
     }
 
 
-def profile_only(which: str, steps: int, warmup: int) -> int:
+def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024) -> int:
     """Launch one kernel `steps` times (after `warmup`) for a profiler run.
 
-    attention:      fp32 causal [8,1024,16,64] (the headline step)
+    attention:      fp32 causal [8,S,16,64], S = --seq-len (1024: the headline step)
     attention_bf16: bf16 causal [1,16384,32,128] (config 5a)
     layernorm:      fp32 residual+LN rows=32768 hidden=4096 (config 3), one input set
     copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
@@ -213,10 +213,10 @@ def profile_only(which: str, steps: int, warmup: int) -> int:
     from transformer_opt.kernels import fused_residual_layer_norm, hip_attention
 
     if which == "attention":
-        q, k, v = make_qkv(8, 1024, 16, 64, torch.float32, seed=1234)
+        q, k, v = make_qkv(8, seq_len, 16, 64, torch.float32, seed=1234)
         out = torch.empty_like(q)
         fn = lambda: hip_attention(q, k, v, causal=True, out=out)  # noqa: E731
-        work = attention_flops(8, 16, 1024, 64, True)
+        work = attention_flops(8, 16, seq_len, 64, True)
     elif which == "attention_bf16":
         q, k, v = make_qkv(1, 16384, 32, 128, torch.bfloat16, seed=5)
         out = torch.empty_like(q)
@@ -272,6 +272,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
+    parser.add_argument("--seq-len", type=int, default=1024,
+                        help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -293,7 +295,7 @@ def main() -> int:
     dev_name = torch.cuda.get_device_name(0)
     log(f"device {dev_name}; library {_native.library_path()}")
     if args.profile_only:
-        return profile_only(args.profile_only, args.steps, args.warmup)
+        return profile_only(args.profile_only, args.steps, args.warmup, args.seq_len)
 
     # ---- headline: config 2, fp32 causal attention, S=1024 -----------------
     B, S, H, D = 8, 1024, 16, 64

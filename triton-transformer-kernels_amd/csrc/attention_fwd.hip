@@ -14,37 +14,51 @@
 //   In the 32x32 MFMA result layout a lane holds one column (query = lane%32)
 //   and 16 rows (keys 8*(r/4) + 4*(lane/32) + r%4 for register r), so
 //     - the softmax row statistics of a query are a reduction over the lane's
-//       own registers plus ONE exchange with lane^32, and
+//       own registers plus ONE exchange with lane^32 (v_permlane32_swap), and
 //     - the probabilities P^T already sit in the B-operand layout of the next
 //       MFMA, O^T[d, query] += V^T[d, key] . P^T[key, query]: register r
 //       feeds the k-step whose two keys are the ones that register holds in
 //       lane halves 0 and 1.  No transpose, no LDS round trip for P.
-// * K and V tiles (BLOCK_N keys) are staged in LDS and double-buffered: the
-//   next tile's global loads are issued before the current tile's MFMAs and
-//   written to the other buffer afterwards, one barrier per tile.  K rows are
-//   padded by 16 bytes, so the 16-byte MFMA operand reads of 16 consecutive
-//   key rows start 4 banks apart and cover all 64 banks without conflict,
-//   and every per-step operand address is the lane's base plus an immediate.
-// * Inside a tile the LDS operand reads are software-pipelined one step ahead
-//   of the MFMAs and fenced with scheduling barriers, which keeps the
-//   register footprint inside the two-waves-per-SIMD budget (no spills).
+// * K and V tiles are double-buffered in LDS with one barrier per tile.  K
+//   rows are padded by 16 bytes, so the 16-byte MFMA operand reads of 16
+//   consecutive key rows start 4 banks apart and cover all 64 banks, and
+//   every per-step operand address is the lane's base plus an immediate.
+//     - fp32: the next tile's global loads are issued into registers before
+//       the current tile's MFMAs and written to the other buffer after them.
+//       The fp32 MFMA is 16 passes long, so the matrix core is the bound and
+//       the softmax VALU of one wavefront runs under the MFMAs of the other
+//       wavefront on the SIMD.
+//     - bf16/fp16: the 8-pass MFMA leaves the softmax VALU (and v_exp_f32,
+//       which does not issue alongside MFMA) as the bound, so the loop is
+//       software-pipelined: iteration t computes S(t) = K(t).Q^T and then one
+//       instruction stream interleaving the P.V MFMAs of tile t-1 with the
+//       softmax of tile t.  K(t+1) is copied global->LDS by LDS-DMA
+//       (global_load_lds_dwordx4, no register staging); V(t) is staged in
+//       registers and stored transposed.
 // * Masking: key validity (key mask and key < S) is a wave-uniform 64-bit
 //   ballot per tile; with the lane's causal limit it becomes one bit mask per
 //   32-key sub-block.  Only tiles that need it (diagonal, ragged end, key
-//   mask) take the masked path; full interior tiles run unmasked.  Causal
+//   mask) take the masked path; interior tiles run unmasked.  Causal
 //   workgroups stop at their diagonal (future tiles are never loaded) and a
 //   wavefront skips the 32-key sub-blocks entirely after its last query.
-// * Scheduling: the flat grid is ordered heaviest query tile first (causal)
-//   and, when B*H is a multiple of 8, all query tiles of one head run on the
-//   same XCD (workgroups are dealt round-robin to the 8 XCDs), so a head's K/V
-//   is fetched from HBM into one XCD's L2 instead of eight.
+// * Scheduling: causal query tile i costs i+1 key blocks.  When the grid
+//   still fills every workgroup slot of the GPU, a workgroup runs the query
+//   tiles nq-1-i and i one after the other, so all workgroups carry the same
+//   nq+1 blocks of work and the launch has no tail.  Otherwise the flat grid
+//   is ordered heaviest query tile first.  When B*H is a multiple of 8 all
+//   workgroups of one head run on the same XCD (workgroups are dealt
+//   round-robin to the 8 XCDs), so a head's K/V is fetched from HBM into one
+//   XCD's L2 instead of eight.
 //
 // fp32 path: v_mfma_f32_32x32x2_f32 (IEEE fp32 products, fp32 accumulate).
 // Q is pre-multiplied by scale*log2(e) so scores are already in the exp2
-// domain.  bf16/fp16 path: v_mfma_f32_32x32x16_{bf16,f16}; scores are kept
-// in fp32 and scaled after the product, P is rounded to the input type for
-// the P.V product, V is stored transposed in LDS so the 16-bit A operand
-// (8 keys of one d) is two 8-byte LDS reads.
+// domain.  bf16/fp16 path: v_mfma_f32_32x32x16_{bf16,f16}; scores stay fp32,
+// the row max is taken on raw scores and the scale is folded into one fma per
+// element before exp2; P is rounded to the input type (v_cvt_pk_bf16_f32 /
+// v_cvt_f16_f32) for the P.V product; V is stored transposed in LDS so the
+// 16-bit A operand (8 keys of one d) is two 8-byte LDS reads.
+#include <atomic>
+
 #include "ttk_common.h"
 
 namespace ttk {
@@ -78,25 +92,61 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Max / sum of a value and the same value in lane ^ 32 (v_permlane32_swap:
+// exchanges the upper half of the first operand with the lower half of the
+// second, so the two results hold {x[l], x[l ^ 32]} in every lane).
+__device__ __forceinline__ float max_with_other_half(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_with_other_half(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// LDS-DMA: each active lane copies 16 bytes from its own global address to
+// lds_base + 16 * lane (global_load_lds_dwordx4; lds_base is wave-uniform).
+// Completion is tracked by vmcnt only: callers wait with vm_wait() before the
+// barrier that publishes the buffer.
+#define TTK_LDS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
+__device__ __forceinline__ void dma16(const void* gptr, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gptr, TTK_LDS(lds_base), 16, 0, 0);
+}
+__device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Key offset (inside a 32-key sub-block) held by register r of lane half h in
 // the 32x32 MFMA result layout.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-// Work item of this workgroup: (query tile, batch*head).
-__device__ __forceinline__ void work_item(const AttnParams& p, bool causal, int& qb, int& bh) {
+// Work of one workgroup: a (batch, head) and one or two query tiles.
+struct Work {
+  int bh;
+  int q_first;   // query tile of the first pass
+  int q_second;  // query tile of the second pass (npass == 2)
+  int npass;
+};
+
+__device__ __forceinline__ Work work_item(const AttnParams& p, bool causal) {
   const int id = blockIdx.x;
-  int qrank;
+  int unit, bh;
   if (p.xcd_swizzle) {
     const int xcd = id & 7;
     const int j = id >> 3;
     const int hpx = p.BH >> 3;  // heads per XCD
-    qrank = j / hpx;
-    bh = xcd + 8 * (j - qrank * hpx);
+    unit = j / hpx;
+    bh = xcd + 8 * (j - unit * hpx);
   } else {
-    qrank = id / p.BH;
-    bh = id - qrank * p.BH;
+    unit = id / p.BH;
+    bh = id - unit * p.BH;
   }
-  qb = causal ? p.nq - 1 - qrank : qrank;
+  Work w;
+  w.bh = bh;
+  w.q_first = causal ? p.nq - 1 - unit : unit;
+  w.q_second = unit;
+  w.npass = (causal && p.pair && unit < w.q_first) ? 2 : 1;
+  return w;
 }
 
 // Valid bits of the keys [k0, k0 + 64) that exist (key < S).
@@ -122,42 +172,25 @@ __device__ __forceinline__ bool reg_allowed(uint32_t a, int r) {
   return (a >> (8 * (r >> 2) + (r & 3))) & 1u;
 }
 
-// Online-softmax update of one tile in the exp2 domain.  `s` holds scaled
-// scores (-inf where not allowed); on return it holds the probabilities.
-template <int NSB, int NACC, bool MASKED>
-__device__ __forceinline__ void online_softmax(f32x16 (&s)[NSB], float& m_run, float& l_run,
-                                               f32x16 (&acc)[NACC]) {
-  float mt = s[0][0];
+// Sets scores of disallowed keys to -inf (tile of NSB sub-blocks from k0).
+template <int NSB, bool CAUSAL>
+__device__ __forceinline__ void apply_mask(f32x16 (&s)[NSB], int k0, uint64_t kvalid, int qrow, int h) {
 #pragma unroll
-  for (int sb = 0; sb < NSB; ++sb)
+  for (int sb = 0; sb < NSB; ++sb) {
+    const uint32_t a =
+        lane_allowed<CAUSAL>(static_cast<uint32_t>(kvalid >> (32 * sb)), k0 + sb * 32, qrow, h);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
-  mt = fmaxf(mt, __shfl_xor(mt, 32));
-  const float m_new = fmaxf(m_run, mt);
-  // A fully masked row keeps m = -inf; use 0 so exp2(-inf - 0) = 0, never NaN.
-  const float m_use = (MASKED && m_new == -INFINITY) ? 0.0f : m_new;
-  const float alpha = fast_exp2(m_run - m_use);
-  float ls = 0.0f;
-#pragma unroll
-  for (int sb = 0; sb < NSB; ++sb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pv = fast_exp2(s[sb][r] - m_use);
-      s[sb][r] = pv;
-      ls += pv;
-    }
-  l_run = __builtin_fmaf(l_run, alpha, ls);
-#pragma unroll
-  for (int i = 0; i < NACC; ++i) acc[i] *= alpha;
-  m_run = m_new;
+    for (int r = 0; r < 16; ++r)
+      if (!reg_allowed(a, r)) s[sb][r] = -INFINITY;
+  }
 }
 
 // Waves per SIMD the register budget is sized for: two workgroups per CU,
-// except where the live state of head_dim 128 (fp32: every variant; 16-bit:
-// non-causal unmasked) does not fit 256 registers without spilling - those
-// run one workgroup per CU with the accumulators in AGPRs.
-template <bool F32, int D, bool CAUSAL, bool HAS_MASK>
-constexpr int kMinWaves = (D >= 128 && (F32 || (!CAUSAL && !HAS_MASK))) ? 1 : 2;
+// except fp32 head_dim 128, whose live state (64 accumulator + 64 Q registers
+// + score tiles + staging) does not fit 256 registers; it runs one workgroup
+// per CU with the accumulators in AGPRs.
+template <bool F32, int D>
+constexpr int kMinWaves = (D >= 128 && F32) ? 1 : 2;
 
 // ----------------------------------------------------------------------------
 // fp32
@@ -188,7 +221,7 @@ struct VFrag32<128> {
 };
 
 template <int D, bool CAUSAL, bool HAS_MASK>
-__global__ __launch_bounds__(kThreads, (kMinWaves<true, D, CAUSAL, HAS_MASK>)) void attn_fwd_f32_kernel(AttnParams p) {
+__global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_kernel(AttnParams p) {
   using C = F32Cfg<D>;
   constexpr int BN = C::BN, NSB = C::NSB, CPR = C::CPR, KS = C::KS, DB = C::DB, CPT = C::CPT,
                 G = C::G;
@@ -197,225 +230,246 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D, CAUSAL, HAS_MASK>)) v
   __shared__ __attribute__((aligned(16))) float smV[2][BN * D];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int m = lane & 31;
   const int h = lane >> 5;
 
-  int qb, bh;
-  work_item(p, CAUSAL, qb, bh);
-  const int b = bh / p.H;
-  const int hh = bh - b * p.H;
+  const Work w = work_item(p, CAUSAL);
+  const int b = w.bh / p.H;
+  const int hh = w.bh - b * p.H;
   const int S = p.S;
   const float* __restrict__ Q = static_cast<const float*>(p.q) + b * p.qb + hh * p.qh;
   const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.kb + hh * p.kh;
   const float* __restrict__ V = static_cast<const float*>(p.v) + b * p.vb + hh * p.vh;
   const uint8_t* __restrict__ M = HAS_MASK ? p.mask + b * p.mb : nullptr;
 
-  const int q0 = qb * kBM + wave * 32;  // first query of this wavefront
-  const int qrow = q0 + m;              // query of this lane
+  // Every pass ends with a barrier after its last LDS read, so the next pass
+  // may refill both buffers right away.
+  for (int pass = 0; pass < w.npass; ++pass) {
+    const int qb = pass == 0 ? w.q_first : w.q_second;
+    const int q0 = qb * kBM + wave * 32;  // first query of this wavefront (uniform)
+    const int qrow = q0 + m;              // query of this lane
 
-  // B operand of S^T = K.Q^T: group g covers d = 8g..8g+7, lane half h holds
-  // d = 8g+4h..8g+4h+3 (one element per k-step).  Pre-scaled into exp2 units.
-  f32x4 qf[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (qrow < S) {
-      qf[g] = *reinterpret_cast<const f32x4*>(Q + qrow * p.qs + 8 * g + 4 * h) * p.scale_log2;
-    } else {
-      qf[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  }
-
-  const int kv_end = CAUSAL ? min(S, (qb + 1) * kBM) : S;
-  const int ntiles = (kv_end + BN - 1) / BN;
-
-  f32x4 rk[CPT], rv[CPT];
-  bool rm = false;
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int idx = tid + kThreads * i;
-      if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
-        const int row = idx / CPR;
-        const int c = idx - row * CPR;
-        const int key = t * BN + row;
-        if (key < S) {
-          rk[i] = *reinterpret_cast<const f32x4*>(K + key * p.ks + 4 * c);
-          rv[i] = *reinterpret_cast<const f32x4*>(V + key * p.vs + 4 * c);
-        } else {
-          rk[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-          rv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-    }
-    if constexpr (HAS_MASK) {
-      const int key = t * BN + lane;  // every wavefront reads the tile's mask bytes
-      rm = lane < BN && key < S && M[key * p.ms] != 0;
-    }
-  };
-  // Writes the staged tile into LDS buffer `buf`; returns the tile's valid-key
-  // bits (key mask and key < S) as a wave-uniform 64-bit mask.
-  auto lstore = [&](int buf, int t) -> uint64_t {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int idx = tid + kThreads * i;
-      if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
-        const int row = idx / CPR;
-        const int c = idx - row * CPR;
-        *reinterpret_cast<f32x4*>(&smK[buf][row * KS + 4 * c]) = rk[i];
-        *reinterpret_cast<f32x4*>(&smV[buf][row * D + 4 * c]) = rv[i];
-      }
-    }
-    if constexpr (HAS_MASK) {
-      return __builtin_amdgcn_ballot_w64(rm);
-    } else {
-      return range_bits(t * BN, S);
-    }
-  };
-
-  auto kread = [&](int buf, int sb, int g) -> f32x4 {
-    const int row = sb * 32 + m;
-    return *reinterpret_cast<const f32x4*>(&smK[buf][row * KS + 8 * g + 4 * h]);
-  };
-  auto vread = [&](int buf, int sb, int r) -> VF {
-    const int krow = sb * 32 + acc_row(r, h);
-    const float* vrow = &smV[buf][krow * D];
-    if constexpr (DB == 1) {
-      return (D >= 32 || m < D) ? vrow[m] : 0.0f;
-    } else {
-      return *reinterpret_cast<const VF*>(vrow + DB * m);
-    }
-  };
-
-  float m_run = -INFINITY;
-  float l_run = 0.0f;  // partial sum over this lane half's keys
-  f32x16 acc[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
-
-  // One tile: S^T = K.Q^T, (mask), online softmax, O^T += V^T.P^T.
-  // `nlive` = number of leading 32-key sub-blocks this wavefront needs.
-  auto tile = [&](auto masked_tag, int buf, int k0, int nlive, uint64_t kvalid) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    f32x16 s[NSB];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
-    // ---- S^T = K . Q^T (K fragments read one group ahead) ----------------
-    f32x4 kf[NSB];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb)
-      if (!MASKED || sb < nlive) kf[sb] = kread(buf, sb, 0);
+    // B operand of S^T = K.Q^T: group g covers d = 8g..8g+7, lane half h
+    // holds d = 8g+4h..8g+4h+3 (one element per k-step).  Pre-scaled into
+    // exp2 units.
+    f32x4 qf[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      f32x4 kn[NSB];
-      if (g + 1 < G) {
-#pragma unroll
-        for (int sb = 0; sb < NSB; ++sb)
-          if (!MASKED || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
-      }
-#pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) {
-        if (MASKED && sb >= nlive) continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kf[sb][e], qf[g][e], s[sb]);
-      }
-      if (g + 1 < G) {
-#pragma unroll
-        for (int sb = 0; sb < NSB; ++sb) kf[sb] = kn[sb];
-      }
-      fence();
-    }
-    // ---- mask ------------------------------------------------------------
-    if constexpr (MASKED) {
-#pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) {
-        const int ks = k0 + sb * 32;
-        const uint32_t a = lane_allowed<CAUSAL>(static_cast<uint32_t>(kvalid >> (32 * sb)), ks, qrow, h);
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (!reg_allowed(a, r)) s[sb][r] = -INFINITY;
-      }
-    }
-    online_softmax<NSB, DB, MASKED>(s, m_run, l_run, acc);
-    fence();
-    // ---- O^T += V^T . P^T (V fragments read one k-step ahead) -------------
-    const int nsteps = (MASKED ? nlive : NSB) * 16;
-    VF vf = vread(buf, 0, 0);
-#pragma unroll
-    for (int idx = 0; idx < NSB * 16; ++idx) {
-      // Fixed trip count (fully unrolled, so s[][] stays in registers); the
-      // masked path skips the k-steps of dead sub-blocks with a uniform guard.
-      if (!MASKED || idx < nsteps) {
-        const int sb = idx >> 4;
-        const int r = idx & 15;
-        VF vn{};
-        if (idx + 1 < NSB * 16 && (!MASKED || idx + 1 < nsteps)) {
-          vn = vread(buf, (idx + 1) >> 4, (idx + 1) & 15);
-        }
-        const float pr = s[sb][r];
-        if constexpr (DB == 1) {
-          acc[0] = mfma_f32(vf, pr, acc[0]);
-        } else if constexpr (DB == 2) {
-          acc[0] = mfma_f32(vf.x, pr, acc[0]);
-          acc[1] = mfma_f32(vf.y, pr, acc[1]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] = mfma_f32(vf[i], pr, acc[i]);
-        }
-        vf = vn;
-      }
-      fence();
-    }
-  };
-
-  gload(0);
-  uint64_t kvalid = lstore(0, 0);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
-    const int k0 = t * BN;
-    if (q0 < S && (!CAUSAL || k0 <= q0 + 31)) {
-      // Leading sub-blocks that hold any key this wavefront may see.
-      int nlive = NSB;
-#pragma unroll
-      for (int sb = NSB - 1; sb >= 0; --sb) {
-        const int ks = k0 + sb * 32;
-        if (ks >= S || (CAUSAL && ks > q0 + 31)) nlive = sb;
-      }
-      const bool need_mask = HAS_MASK || (k0 + BN > S) || (CAUSAL && k0 + BN - 1 > q0);
-      if (need_mask) {
-        tile(std::true_type{}, buf, k0, nlive, kvalid);
+      if (qrow < S) {
+        qf[g] = *reinterpret_cast<const f32x4*>(Q + qrow * p.qs + 8 * g + 4 * h) * p.scale_log2;
       } else {
-        tile(std::false_type{}, buf, k0, NSB, kvalid);
+        qf[g] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    if (t + 1 < ntiles) kvalid = lstore(buf ^ 1, t + 1);
-    __syncthreads();
-  }
 
-  // ---- epilogue: O = acc / l ------------------------------------------------
-  const float lt = l_run + __shfl_xor(l_run, 32);
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  if (qrow >= S) return;
-  float* __restrict__ O = static_cast<float*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
+    const int kv_end = CAUSAL ? min(S, (qb + 1) * kBM) : S;
+    const int ntiles = (kv_end + BN - 1) / BN;
+
+    f32x4 rk[CPT], rv[CPT];
+    bool rm = false;
+    // Global loads of tile t into registers; rows past S read as zeros.
+    auto gload = [&](int t) {
+      const bool full = (t + 1) * BN <= S;
 #pragma unroll
-  for (int j4 = 0; j4 < 4; ++j4) {
-    // Block i of the accumulator holds d = DB*row + i; register 4*j4+e holds
-    // row 8*j4 + 4h + e, so a lane's d-values form one run of 4*DB.
-    const int d0 = DB * (8 * j4 + 4 * h);
-    if (D < 32 && d0 >= D) continue;
-    float vals[4 * DB];
+      for (int i = 0; i < CPT; ++i) {
+        const int idx = tid + kThreads * i;
+        if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
+          const int row = idx / CPR;
+          const int c = idx - row * CPR;
+          const int key = t * BN + row;
+          if (full || key < S) {
+            rk[i] = *reinterpret_cast<const f32x4*>(K + key * p.ks + 4 * c);
+            rv[i] = *reinterpret_cast<const f32x4*>(V + key * p.vs + 4 * c);
+          } else {
+            rk[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            rv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+      if constexpr (HAS_MASK) {
+        const int key = t * BN + lane;  // every wavefront reads the tile's mask bytes
+        rm = lane < BN && key < S && M[key * p.ms] != 0;
+      }
+    };
+    // Writes the staged tile into LDS buffer `buf`; returns the tile's
+    // valid-key bits (key mask and key < S) as a wave-uniform 64-bit mask.
+    auto lstore = [&](int buf, int t) -> uint64_t {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+      for (int i = 0; i < CPT; ++i) {
+        const int idx = tid + kThreads * i;
+        if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
+          const int row = idx / CPR;
+          const int c = idx - row * CPR;
+          *reinterpret_cast<f32x4*>(&smK[buf][row * KS + 4 * c]) = rk[i];
+          *reinterpret_cast<f32x4*>(&smV[buf][row * D + 4 * c]) = rv[i];
+        }
+      }
+      if constexpr (HAS_MASK) {
+        return __builtin_amdgcn_ballot_w64(rm);
+      } else {
+        return range_bits(t * BN, S);
+      }
+    };
+
+    auto kread = [&](int buf, int sb, int g) -> f32x4 {
+      const int row = sb * 32 + m;
+      return *reinterpret_cast<const f32x4*>(&smK[buf][row * KS + 8 * g + 4 * h]);
+    };
+    auto vread = [&](int buf, int sb, int r) -> VF {
+      const int krow = sb * 32 + acc_row(r, h);
+      const float* vrow = &smV[buf][krow * D];
+      if constexpr (DB == 1) {
+        return (D >= 32 || m < D) ? vrow[m] : 0.0f;
+      } else {
+        return *reinterpret_cast<const VF*>(vrow + DB * m);
+      }
+    };
+
+    float m_run = -INFINITY;
+    float l_run = 0.0f;  // partial sum over this lane half's keys
+    f32x16 acc[DB];
 #pragma unroll
-      for (int i = 0; i < DB; ++i) vals[DB * e + i] = acc[i][4 * j4 + e] * inv;
+    for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
+
+    // One tile: S^T = K.Q^T, (mask), online softmax, O^T += V^T.P^T.
+    // `nlive` = number of leading 32-key sub-blocks this wavefront needs.
+    auto tile = [&](auto masked_tag, int buf, int k0, int nlive, uint64_t kvalid) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      f32x16 s[NSB];
 #pragma unroll
-    for (int c = 0; c < DB; ++c) {
-      *reinterpret_cast<f32x4*>(O + d0 + 4 * c) =
-          f32x4{vals[4 * c], vals[4 * c + 1], vals[4 * c + 2], vals[4 * c + 3]};
+      for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
+      // ---- S^T = K . Q^T (K fragments read one group ahead) --------------
+      f32x4 kf[NSB];
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+        if (!MASKED || sb < nlive) kf[sb] = kread(buf, sb, 0);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        f32x4 kn[NSB];
+        if (g + 1 < G) {
+#pragma unroll
+          for (int sb = 0; sb < NSB; ++sb)
+            if (!MASKED || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
+        }
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          if (MASKED && sb >= nlive) continue;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kf[sb][e], qf[g][e], s[sb]);
+        }
+        if (g + 1 < G) {
+#pragma unroll
+          for (int sb = 0; sb < NSB; ++sb) kf[sb] = kn[sb];
+        }
+        fence();
+      }
+      if constexpr (MASKED) apply_mask<NSB, CAUSAL>(s, k0, kvalid, qrow, h);
+      // ---- online softmax (exp2 domain) ------------------------------------
+      float mt = s[0][0];
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
+      mt = max_with_other_half(mt);
+      const float m_new = fmaxf(m_run, mt);
+      // A fully masked row keeps m = -inf; use 0 so exp2(-inf - 0) = 0, never NaN.
+      const float m_use = (MASKED && m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = fast_exp2(m_run - m_use);
+      float ls = 0.0f;
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pr = fast_exp2(s[sb][r] - m_use);
+          s[sb][r] = pr;
+          ls += pr;
+        }
+      l_run = __builtin_fmaf(l_run, alpha, ls);
+#pragma unroll
+      for (int i = 0; i < DB; ++i) acc[i] *= alpha;
+      m_run = m_new;
+      fence();
+      // ---- O^T += V^T . P^T (V fragments read one k-step ahead) -----------
+      const int nsteps = (MASKED ? nlive : NSB) * 16;
+      VF vf = vread(buf, 0, 0);
+#pragma unroll
+      for (int idx = 0; idx < NSB * 16; ++idx) {
+        // Fixed trip count (fully unrolled, so s[][] stays in registers); the
+        // masked path skips the k-steps of dead sub-blocks with a uniform guard.
+        if (!MASKED || idx < nsteps) {
+          const int sb = idx >> 4;
+          const int r = idx & 15;
+          VF vn{};
+          if (idx + 1 < NSB * 16 && (!MASKED || idx + 1 < nsteps)) {
+            vn = vread(buf, (idx + 1) >> 4, (idx + 1) & 15);
+          }
+          const float pr = s[sb][r];
+          if constexpr (DB == 1) {
+            acc[0] = mfma_f32(vf, pr, acc[0]);
+          } else if constexpr (DB == 2) {
+            acc[0] = mfma_f32(vf.x, pr, acc[0]);
+            acc[1] = mfma_f32(vf.y, pr, acc[1]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = mfma_f32(vf[i], pr, acc[i]);
+          }
+          vf = vn;
+        }
+        fence();
+      }
+    };
+
+    gload(0);
+    uint64_t kvalid = lstore(0, 0);
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+      const int buf = t & 1;
+      if (t + 1 < ntiles) gload(t + 1);
+      const int k0 = t * BN;
+      if (q0 < S && (!CAUSAL || k0 <= q0 + 31)) {
+        // Leading sub-blocks that hold any key this wavefront may see.
+        int nlive = NSB;
+#pragma unroll
+        for (int sb = NSB - 1; sb >= 0; --sb) {
+          const int ks = k0 + sb * 32;
+          if (ks >= S || (CAUSAL && ks > q0 + 31)) nlive = sb;
+        }
+        const bool need_mask = HAS_MASK || (k0 + BN > S) || (CAUSAL && k0 + BN - 1 > q0);
+        if (need_mask) {
+          tile(std::true_type{}, buf, k0, nlive, kvalid);
+        } else {
+          tile(std::false_type{}, buf, k0, NSB, kvalid);
+        }
+      }
+      if (t + 1 < ntiles) kvalid = lstore(buf ^ 1, t + 1);
+      __syncthreads();
+    }
+
+    // ---- epilogue: O = acc / l ----------------------------------------------
+    const float lt = sum_with_other_half(l_run);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (qrow < S) {
+      float* __restrict__ O = static_cast<float*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        // Block i of the accumulator holds d = DB*row + i; register 4*j4+e
+        // holds row 8*j4 + 4h + e, so a lane's d-values form one run of 4*DB.
+        const int d0 = DB * (8 * j4 + 4 * h);
+        if (D < 32 && d0 >= D) continue;
+        float vals[4 * DB];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < DB; ++i) vals[DB * e + i] = acc[i][4 * j4 + e] * inv;
+#pragma unroll
+        for (int c = 0; c < DB; ++c) {
+          *reinterpret_cast<f32x4*>(O + d0 + 4 * c) =
+              f32x4{vals[4 * c], vals[4 * c + 1], vals[4 * c + 2], vals[4 * c + 3]};
+        }
+      }
     }
   }
 }
@@ -433,31 +487,29 @@ struct H16Cfg {
   static constexpr int NDB = (D + 31) / 32;          // output blocks of 32 d-rows
   static constexpr int G = DK / 16;                  // Q.K k-steps of 16
   static constexpr int VTS = BN + 4;                 // V^T row stride (elements)
-  static constexpr int CHUNKS = BN * CPR;
-  static constexpr int CPT = (CHUNKS + kThreads - 1) / kThreads;
   // V^T store: a thread moves 4 keys x 8 d (four 16-byte global loads).
   static constexpr int VGROUPS = (BN / 4) * CPR;
   static constexpr int VPT = (VGROUPS + kThreads - 1) / kThreads;
+  static constexpr int NSTEP = NSB * 2 * NDB;        // P.V MFMAs per tile
 };
 
 template <typename T, int D, bool CAUSAL, bool HAS_MASK>
-__global__ __launch_bounds__(kThreads, (kMinWaves<false, D, CAUSAL, HAS_MASK>)) void attn_fwd_h16_kernel(AttnParams p) {
+__global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_kernel(AttnParams p) {
   using C = H16Cfg<D>;
-  constexpr int BN = C::BN, NSB = C::NSB, CPR = C::CPR, DK = C::DK, KS = C::KS,
-                NDB = C::NDB, VTS = C::VTS, CPT = C::CPT, VPT = C::VPT, G = C::G;
+  constexpr int BN = C::BN, NSB = C::NSB, CPR = C::CPR, KS = C::KS,
+                NDB = C::NDB, VTS = C::VTS, VPT = C::VPT, G = C::G, NSTEP = C::NSTEP;
   __shared__ __attribute__((aligned(16))) unsigned short smK[2][BN * KS];
   __shared__ __attribute__((aligned(16))) unsigned short smVt[2][D * VTS];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int m = lane & 31;
   const int h = lane >> 5;
 
-  int qb, bh;
-  work_item(p, CAUSAL, qb, bh);
-  const int b = bh / p.H;
-  const int hh = bh - b * p.H;
+  const Work w = work_item(p, CAUSAL);
+  const int b = w.bh / p.H;
+  const int hh = w.bh - b * p.H;
   const int S = p.S;
   using St = unsigned short;
   const St* __restrict__ Q = static_cast<const St*>(p.q) + b * p.qb + hh * p.qh;
@@ -465,241 +517,392 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D, CAUSAL, HAS_MASK>)) 
   const St* __restrict__ V = static_cast<const St*>(p.v) + b * p.vb + hh * p.vh;
   const uint8_t* __restrict__ M = HAS_MASK ? p.mask + b * p.mb : nullptr;
 
-  const int q0 = qb * kBM + wave * 32;
-  const int qrow = q0 + m;
+  // The row max is taken on raw scores, which needs a positive scale: a
+  // negative scale is folded into Q as an exact sign flip.
+  const bool negate = p.scale_log2 < 0.0f;
+  const float c = negate ? -p.scale_log2 : p.scale_log2;
+  const unsigned short sign = negate ? 0x8000u : 0u;
 
-  // B operand of S^T = K.Q^T: k-step g covers d = 16g..16g+15, lane half h
-  // holds d = 16g+8h..16g+8h+7.
-  u16x8 qf[G];
+  // K: LDS-DMA into padded rows of KCH 16-byte chunks; DMA instruction j
+  // fills chunks [64j, 64j + 64) and the instructions are dealt round-robin
+  // to the wavefronts.  A lane landing on the pad chunk - and for head_dim 8
+  // on the zero-padded d 8..15, which meets zero Q entries - copies chunk 0
+  // again; keys past S copy row S-1 (finite data that the mask neutralises).
+  // The (row, chunk) a lane copies is the same for every tile, so its element
+  // offset is computed once (row < 64 and the ABI bounds the key stride below
+  // 2^25 elements, so it fits int32); -1 marks a lane past the tile.
+  constexpr int KCH = KS / 8;
+  constexpr int NK = (BN * KCH + 63) / 64;
+  constexpr int NW = kThreads / 64;
+  constexpr int KPW = (NK + NW - 1) / NW;
+  int koff[KPW];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int d = 16 * g + 8 * h;
-    if (qrow < S && d < D) {
-      qf[g] = *reinterpret_cast<const u16x8*>(Q + qrow * p.qs + d);
-    } else {
-      qf[g] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+  for (int i = 0; i < KPW; ++i) {
+    const int pos = 64 * (wave + NW * i) + lane;
+    const int row = pos / KCH;
+    const int cc = pos - row * KCH;
+    koff[i] = pos < BN * KCH ? row * static_cast<int>(p.ks) + 8 * (cc < CPR ? cc : 0) : -1;
   }
 
-  const int kv_end = CAUSAL ? min(S, (qb + 1) * kBM) : S;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  {
+    // 16-bit workgroups run one query tile (never paired: a second pass costs
+    // this kernel more in register pressure than it gains in balance).
+    const int qb = w.q_first;
+    const int q0 = qb * kBM + wave * 32;
+    const int qrow = q0 + m;
 
-  // K: CPT chunks of 8 elements per thread.  V: VPT groups of 4 keys x 8 d.
-  u32x4 rk[CPT];
-  u32x4 rv[VPT][4];
-  bool rm = false;
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int idx = tid + kThreads * i;
-      if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
-        const int row = idx / CPR;
-        const int c = idx - row * CPR;
-        const int key = t * BN + row;
-        rk[i] = key < S ? *reinterpret_cast<const u32x4*>(K + key * p.ks + 8 * c)
-                        : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int gi = tid + kThreads * i;
-      if (C::VGROUPS % kThreads == 0 || gi < C::VGROUPS) {
-        const int kq = gi / CPR;  // key quad
-        const int c = gi - kq * CPR;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = t * BN + 4 * kq + e;
-          rv[i][e] = key < S ? *reinterpret_cast<const u32x4*>(V + key * p.vs + 8 * c)
-                             : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-    }
-    if constexpr (HAS_MASK) {
-      const int key = t * BN + lane;
-      rm = lane < BN && key < S && M[key * p.ms] != 0;
-    }
-  };
-  auto lstore = [&](int buf, int t) -> uint64_t {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int idx = tid + kThreads * i;
-      if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
-        const int row = idx / CPR;
-        const int c = idx - row * CPR;
-        *reinterpret_cast<u32x4*>(&smK[buf][row * KS + 8 * c]) = rk[i];
-      }
-    }
-    if constexpr (DK != D) {
-      // Zero the padded tail of each K row (head_dim 8): logical chunk 1.
-      if (tid < BN) {
-        const int row = tid;
-        *reinterpret_cast<u32x4*>(&smK[buf][row * KS + 8]) =
-            u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int gi = tid + kThreads * i;
-      if (C::VGROUPS % kThreads == 0 || gi < C::VGROUPS) {
-        const int kq = gi / CPR;
-        const int c = gi - kq * CPR;
-        // Transpose 4 keys x 8 d into 8 rows of V^T (4 consecutive keys each).
-#pragma unroll
-        for (int dd = 0; dd < 8; ++dd) {
-          const int word = dd >> 1;
-          const int shift = (dd & 1) * 16;
-          u32x2 packed;
-          packed[0] = ((rv[i][0][word] >> shift) & 0xffffu) | (((rv[i][1][word] >> shift) & 0xffffu) << 16);
-          packed[1] = ((rv[i][2][word] >> shift) & 0xffffu) | (((rv[i][3][word] >> shift) & 0xffffu) << 16);
-          *reinterpret_cast<u32x2*>(&smVt[buf][(8 * c + dd) * VTS + 4 * kq]) = packed;
-        }
-      }
-    }
-    if constexpr (HAS_MASK) {
-      return __builtin_amdgcn_ballot_w64(rm);
-    } else {
-      return range_bits(t * BN, S);
-    }
-  };
-
-  auto kread = [&](int buf, int sb, int g) -> u16x8 {
-    const int row = sb * 32 + m;
-    return *reinterpret_cast<const u16x8*>(&smK[buf][row * KS + 16 * g + 8 * h]);
-  };
-  // A operand of the P.V k-step (sb, j) for d-block db: keys
-  // sb*32 + 16j + 4h + {0..3} and sb*32 + 16j + 8 + 4h + {0..3} of d-row d.
-  auto vread = [&](int buf, int sb, int j, int db) -> u16x8 {
-    const int d = 32 * db + m;
-    if (D < 32 && d >= D) return u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    const int kbase = sb * 32 + 16 * j + 4 * h;
-    const u16x4 lo = *reinterpret_cast<const u16x4*>(&smVt[buf][d * VTS + kbase]);
-    const u16x4 hi = *reinterpret_cast<const u16x4*>(&smVt[buf][d * VTS + kbase + 8]);
-    return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  };
-
-  float m_run = -INFINITY;
-  float l_run = 0.0f;
-  f32x16 acc[NDB];
-#pragma unroll
-  for (int i = 0; i < NDB; ++i) acc[i] = f32x16{};
-
-  auto tile = [&](auto masked_tag, int buf, int k0, int nlive, uint64_t kvalid) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    f32x16 s[NSB];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
-    u16x8 kf[NSB];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb)
-      if (!MASKED || sb < nlive) kf[sb] = kread(buf, sb, 0);
+    // B operand of S^T = K.Q^T: k-step g covers d = 16g..16g+15, lane half h
+    // holds d = 16g+8h..16g+8h+7.
+    u16x8 qf[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      u16x8 kn[NSB];
-      if (g + 1 < G) {
-#pragma unroll
-        for (int sb = 0; sb < NSB; ++sb)
-          if (!MASKED || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
-      }
-#pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) {
-        if (MASKED && sb >= nlive) continue;
-        s[sb] = mfma_16(T{}, kf[sb], qf[g], s[sb]);
-      }
-      if (g + 1 < G) {
-#pragma unroll
-        for (int sb = 0; sb < NSB; ++sb) kf[sb] = kn[sb];
-      }
-      fence();
-    }
-    // Scores to the exp2 domain (fp32, after the product).
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) s[sb] *= p.scale_log2;
-    if constexpr (MASKED) {
-#pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) {
-        const int ks = k0 + sb * 32;
-        const uint32_t a = lane_allowed<CAUSAL>(static_cast<uint32_t>(kvalid >> (32 * sb)), ks, qrow, h);
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (!reg_allowed(a, r)) s[sb][r] = -INFINITY;
+      const int d = 16 * g + 8 * h;
+      if (qrow < S && d < D) {
+        qf[g] = *reinterpret_cast<const u16x8*>(Q + qrow * p.qs + d) ^ sign;
+      } else {
+        qf[g] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
-    online_softmax<NSB, NDB, MASKED>(s, m_run, l_run, acc);
-    // P^T in the B-operand layout of the 32x32x16 MFMA: k-step (sb, j) takes
-    // registers 8j..8j+7, i.e. keys 16j+4h+{0..3} and 16j+8+4h+{0..3}.
-    u16x8 pk[NSB][2];
+
+    const int kv_end = CAUSAL ? min(S, (qb + 1) * kBM) : S;
+    const int ntiles = (kv_end + BN - 1) / BN;
+
+    u32x4 rv[VPT][4];
+    bool rm = false;
+    auto dma_k = [&](int buf, int t) __attribute__((always_inline)) {
+      if constexpr (HAS_MASK) {
+        const int key = t * BN + lane;
+        rm = lane < BN && key < S && M[key * p.ms] != 0;
+      }
+      const St* kt = K + static_cast<int64_t>(t) * BN * p.ks;
+      const bool ragged = (t + 1) * BN > S;
 #pragma unroll
-    for (int sb = 0; sb < NSB; ++sb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) pk[sb][r >> 3][r & 7] = to_bits(T{}, s[sb][r]);
-    fence();
-    constexpr int NSTEP = NSB * 2 * NDB;
-    const int nsteps = (MASKED ? nlive : NSB) * 2 * NDB;
-    u16x8 vf = vread(buf, 0, 0, 0);
-#pragma unroll
-    for (int idx = 0; idx < NSTEP; ++idx) {
-      if (!MASKED || idx < nsteps) {
-        const int db = idx % NDB;
-        const int j = (idx / NDB) & 1;
-        const int sb = idx / (2 * NDB);
-        u16x8 vn{};
-        const int nx = idx + 1;
-        if (nx < NSTEP && (!MASKED || nx < nsteps)) {
-          vn = vread(buf, nx / (2 * NDB), (nx / NDB) & 1, nx % NDB);
+      for (int i = 0; i < KPW; ++i) {
+        const int j = wave + NW * i;
+        if (j < NK && koff[i] >= 0) {
+          if (!ragged) {
+            dma16(kt + koff[i], &smK[buf][512 * j]);
+          } else {
+            const int pos = 64 * j + lane;
+            const int row = pos / KCH;
+            const int cc = pos - row * KCH;
+            const int key = min(t * BN + row, S - 1);
+            dma16(K + key * p.ks + 8 * (cc < CPR ? cc : 0), &smK[buf][512 * j]);
+          }
         }
-        acc[db] = mfma_16(T{}, vf, pk[sb][j], acc[db]);
-        vf = vn;
       }
-      fence();
-    }
-  };
+    };
+    // Valid-key bits (key mask and key < S) of tile t as a wave-uniform mask;
+    // with a key mask, call after vm_wait() (the mask bytes load in dma_k).
+    auto key_bits = [&](int t) __attribute__((always_inline)) -> uint64_t {
+      if constexpr (HAS_MASK) {
+        return __builtin_amdgcn_ballot_w64(rm);
+      } else {
+        return range_bits(t * BN, S);
+      }
+    };
+    // V: VPT groups of 4 keys x 8 d per thread, staged in registers and
+    // transposed on the LDS store; keys past S read as zeros.
+    auto gload_v = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int gi = tid + kThreads * i;
+        if (C::VGROUPS % kThreads == 0 || gi < C::VGROUPS) {
+          const int kq = gi / CPR;  // key quad
+          const int cc = gi - kq * CPR;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = t * BN + 4 * kq + e;
+            rv[i][e] = key < S ? *reinterpret_cast<const u32x4*>(V + key * p.vs + 8 * cc)
+                               : u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+      }
+    };
+    auto lstore_v = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int gi = tid + kThreads * i;
+        if (C::VGROUPS % kThreads == 0 || gi < C::VGROUPS) {
+          const int kq = gi / CPR;
+          const int cc = gi - kq * CPR;
+          // Transpose 4 keys x 8 d into 8 rows of V^T (4 consecutive keys each).
+#pragma unroll
+          for (int dd = 0; dd < 8; ++dd) {
+            const int word = dd >> 1;
+            const int shift = (dd & 1) * 16;
+            u32x2 packed;
+            packed[0] = ((rv[i][0][word] >> shift) & 0xffffu) | (((rv[i][1][word] >> shift) & 0xffffu) << 16);
+            packed[1] = ((rv[i][2][word] >> shift) & 0xffffu) | (((rv[i][3][word] >> shift) & 0xffffu) << 16);
+            *reinterpret_cast<u32x2*>(&smVt[buf][(8 * cc + dd) * VTS + 4 * kq]) = packed;
+          }
+        }
+      }
+    };
 
-  gload(0);
-  uint64_t kvalid = lstore(0, 0);
-  __syncthreads();
+    auto kread = [&](int buf, int sb, int g) __attribute__((always_inline)) -> u16x8 {
+      const int row = sb * 32 + m;
+      return *reinterpret_cast<const u16x8*>(&smK[buf][row * KS + 16 * g + 8 * h]);
+    };
+    // A operand of P.V step idx = ((sb * 2 + j) * NDB + db): d-row 32*db + m,
+    // keys sb*32 + 16j + 4h + {0..3} and sb*32 + 16j + 8 + 4h + {0..3}.
+    auto vread = [&](int buf, int idx) __attribute__((always_inline)) -> u16x8 {
+      const int db = idx % NDB;
+      const int kstep = idx / NDB;  // sb * 2 + j
+      const int d = 32 * db + m;
+      if (D < 32 && d >= D) return u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      const int kbase = 16 * kstep + 4 * h;
+      const u16x4 lo = *reinterpret_cast<const u16x4*>(&smVt[buf][d * VTS + kbase]);
+      const u16x4 hi = *reinterpret_cast<const u16x4*>(&smVt[buf][d * VTS + kbase + 8]);
+      return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
-    const int k0 = t * BN;
-    if (q0 < S && (!CAUSAL || k0 <= q0 + 31)) {
+    float m_run = -INFINITY;  // running max of RAW scores
+    float l_run = 0.0f;
+    f32x16 acc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) acc[i] = f32x16{};
+    // Probabilities of the pending tile in the B-operand layout of the
+    // 32x32x16 MFMA: k-step (sb, j) takes registers 8j..8j+7 of sub-block sb,
+    // i.e. keys 16j+4h+{0..3} and 16j+8+4h+{0..3}.
+    u16x8 pk[NSB * 2];
+#pragma unroll
+    for (int i = 0; i < NSB * 2; ++i) pk[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+
+    auto qk = [&](auto masked_tag, int buf, int nlive, f32x16 (&s)[NSB]) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
+      u16x8 kf[NSB];
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+        if (!MASKED || sb < nlive) kf[sb] = kread(buf, sb, 0);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        u16x8 kn[NSB];
+        if (g + 1 < G) {
+#pragma unroll
+          for (int sb = 0; sb < NSB; ++sb)
+            if (!MASKED || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
+        }
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          if (MASKED && sb >= nlive) continue;
+          s[sb] = mfma_16(T{}, kf[sb], qf[g], s[sb]);
+        }
+        if (g + 1 < G) {
+#pragma unroll
+          for (int sb = 0; sb < NSB; ++sb) kf[sb] = kn[sb];
+        }
+        fence();
+      }
+    };
+
+    auto pv = [&](int buf, int nlive) __attribute__((always_inline)) {
+      const int nsteps = nlive * 2 * NDB;
+      u16x8 vf = vread(buf, 0);
+#pragma unroll
+      for (int idx = 0; idx < NSTEP; ++idx) {
+        if (idx < nsteps) {
+          u16x8 vn{};
+          if (idx + 1 < NSTEP && idx + 1 < nsteps) vn = vread(buf, idx + 1);
+          acc[idx % NDB] = mfma_16(T{}, vf, pk[idx / NDB], acc[idx % NDB]);
+          vf = vn;
+        }
+        fence();
+      }
+    };
+
+    auto softmax = [&](auto masked_tag, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      float mt = s[0][0];
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
+      mt = max_with_other_half(mt);
+      const float m_new = fmaxf(m_run, mt);
+      const float m_use = (MASKED && m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = fast_exp2((m_run - m_use) * c);
+      const float mc = m_use * c;
+      float ls = 0.0f;
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pr = fast_exp2(__builtin_fmaf(s[sb][r], c, -mc));
+          ls += pr;
+          pn[sb * 2 + (r >> 3)][r & 7] = to_bits(T{}, pr);
+        }
+      l_run = __builtin_fmaf(l_run, alpha, ls);
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
+      m_run = m_new;
+    };
+
+    // P.V of the pending tile interleaved with the softmax of s: the first
+    // half of the k-steps carries the row max, the second half the exp2 /
+    // running sum / conversion.
+    auto fused = [&](auto masked_tag, int buf, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr int HALF = NSTEP / 2;
+      constexpr int E = NSB * 16;      // score elements per lane
+      constexpr int PER = E / HALF;    // elements per step in each phase
+      float mt = -INFINITY;
+      float ls = 0.0f, m_new = 0.0f, m_use = 0.0f, alpha = 0.0f, mc = 0.0f;
+      u16x8 vf = vread(buf, 0);
+#pragma unroll
+      for (int idx = 0; idx < NSTEP; ++idx) {
+        u16x8 vn{};
+        if (idx + 1 < NSTEP) vn = vread(buf, idx + 1);
+        acc[idx % NDB] = mfma_16(T{}, vf, pk[idx / NDB], acc[idx % NDB]);
+        if (idx < HALF) {
+#pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int e = PER * idx + j;
+            mt = fmaxf(mt, s[e >> 4][e & 15]);
+          }
+          if (idx == HALF - 1) {
+            mt = max_with_other_half(mt);
+            m_new = fmaxf(m_run, mt);
+            m_use = (MASKED && m_new == -INFINITY) ? 0.0f : m_new;
+            alpha = fast_exp2((m_run - m_use) * c);
+            mc = m_use * c;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int e = PER * (idx - HALF) + j;
+            const float pr = fast_exp2(__builtin_fmaf(s[e >> 4][e & 15], c, -mc));
+            ls += pr;
+            pn[(e >> 4) * 2 + ((e & 15) >> 3)][e & 7] = to_bits(T{}, pr);
+          }
+        }
+        vf = vn;
+        fence();
+      }
+      l_run = __builtin_fmaf(l_run, alpha, ls);
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
+      m_run = m_new;
+    };
+
+    dma_k(0, 0);
+    vm_wait();
+    uint64_t kvalid = key_bits(0);
+    __syncthreads();
+
+    // Tiles [0, n_full) of this wavefront are "full": every sub-block live,
+    // no causal or ragged-end masking (a key mask may still apply).  Tiles
+    // [1, n_full) run the branch-free steady body; tile 0 and the tail use
+    // the generic body.  Both execute one barrier per tile, so all
+    // wavefronts meet ntiles barriers.
+    const int n_full = q0 >= S ? 0 : min(min(ntiles, S / BN), CAUSAL ? (q0 + 1) / BN : ntiles);
+    bool pending = false;  // a tile's P.V is still to be accumulated (uniform)
+    int pend_live = 0;     // its number of live sub-blocks
+
+    auto finish_tile = [&](int t, int kb) __attribute__((always_inline)) {
+      lstore_v(kb);
+      vm_wait();
+      const uint64_t kvalid_next = key_bits(t + 1);
+      __syncthreads();
+      kvalid = kvalid_next;
+    };
+    auto generic_tile = [&](int t) __attribute__((always_inline)) {
+      const int kb = t & 1;
+      // K(t+1) goes to the buffer K(t-1) used, V(t) to the one V(t-2) used;
+      // neither is read in this iteration.
+      if (t + 1 < ntiles) dma_k(kb ^ 1, t + 1);
+      gload_v(t);
+      const int k0 = t * BN;
+      const bool live = q0 < S && (!CAUSAL || k0 <= q0 + 31);
       int nlive = NSB;
 #pragma unroll
       for (int sb = NSB - 1; sb >= 0; --sb) {
         const int ks = k0 + sb * 32;
         if (ks >= S || (CAUSAL && ks > q0 + 31)) nlive = sb;
       }
-      const bool need_mask = HAS_MASK || (k0 + BN > S) || (CAUSAL && k0 + BN - 1 > q0);
-      if (need_mask) {
-        tile(std::true_type{}, buf, k0, nlive, kvalid);
-      } else {
-        tile(std::false_type{}, buf, k0, NSB, kvalid);
+      if (pending) pv(kb ^ 1, pend_live);
+      if (live) {
+        f32x16 s[NSB];
+        u16x8 pn[NSB * 2];
+        qk(std::true_type{}, kb, nlive, s);
+        apply_mask<NSB, CAUSAL>(s, k0, kvalid, qrow, h);
+        softmax(std::true_type{}, s, pn);
+#pragma unroll
+        for (int i = 0; i < NSB * 2; ++i) pk[i] = pn[i];
+        pend_live = nlive;
       }
-    }
-    if (t + 1 < ntiles) kvalid = lstore(buf ^ 1, t + 1);
-    __syncthreads();
-  }
+      pending = live;
+      finish_tile(t, kb);
+    };
 
-  const float lt = l_run + __shfl_xor(l_run, 32);
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  if (qrow >= S) return;
-  St* __restrict__ O = static_cast<St*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
+    generic_tile(0);
+    for (int t = 1; t < n_full; ++t) {
+      const int kb = t & 1;
+      if (t + 1 < ntiles) dma_k(kb ^ 1, t + 1);
+      gload_v(t);
+      f32x16 s[NSB];
+      u16x8 pn[NSB * 2];
+      qk(std::false_type{}, kb, NSB, s);
+      if constexpr (HAS_MASK) {
+        apply_mask<NSB, false>(s, t * BN, kvalid, qrow, h);
+        fused(std::true_type{}, kb ^ 1, s, pn);
+      } else {
+        fused(std::false_type{}, kb ^ 1, s, pn);
+      }
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int j4 = 0; j4 < 4; ++j4) {
-      const int d0 = 32 * db + 8 * j4 + 4 * h;  // 4 consecutive d-rows
-      if (D < 32 && d0 >= D) continue;
-      u16x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = to_bits(T{}, acc[db][4 * j4 + e] * inv);
-      *reinterpret_cast<u16x4*>(O + d0) = o;
+      for (int i = 0; i < NSB * 2; ++i) pk[i] = pn[i];
+      finish_tile(t, kb);
     }
+    for (int t = max(1, n_full); t < ntiles; ++t) generic_tile(t);
+    if (pending) pv((ntiles - 1) & 1, pend_live);
+
+    const float lt = sum_with_other_half(l_run);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (qrow < S) {
+      St* __restrict__ O = static_cast<St*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+          const int d0 = 32 * db + 8 * j4 + 4 * h;  // 4 consecutive d-rows
+          if (D < 32 && d0 >= D) continue;
+          u16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = to_bits(T{}, acc[db][4 * j4 + e] * inv);
+          *reinterpret_cast<u16x4*>(O + d0) = o;
+        }
+    }
+  }
+}
+
+// Compute units of the current device (queried once per device).
+int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      n = 256;
+    }
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 template <int D, bool CAUSAL, bool HAS_MASK>
-hipError_t launch_d(int dtype, const AttnParams& p, int grid, hipStream_t stream) {
-  const dim3 g(static_cast<unsigned>(grid)), blk(kThreads);
+hipError_t launch_d(int dtype, AttnParams& p, hipStream_t stream) {
+  // Causal pairing (fp32 kernel only) halves the grid; use it only while the
+  // paired grid still gives every workgroup slot of the GPU (CUs x resident
+  // workgroups) one workgroup - below that, the tail of the unpaired grid is
+  // cheaper than idle slots.
+  const int64_t paired = static_cast<int64_t>((p.nq + 1) / 2) * p.BH;
+  p.pair = (dtype == 0 && CAUSAL && p.nq >= 2 &&
+            paired >= static_cast<int64_t>(device_cu_count()) * kMinWaves<true, D>) ? 1 : 0;
+  p.units = p.pair ? (p.nq + 1) / 2 : p.nq;
+  const dim3 g(static_cast<unsigned>(p.units) * static_cast<unsigned>(p.BH)), blk(kThreads);
   switch (dtype) {
     case 0: attn_fwd_f32_kernel<D, CAUSAL, HAS_MASK><<<g, blk, 0, stream>>>(p); break;
     case 1: attn_fwd_h16_kernel<BF16, D, CAUSAL, HAS_MASK><<<g, blk, 0, stream>>>(p); break;
@@ -710,28 +913,27 @@ hipError_t launch_d(int dtype, const AttnParams& p, int grid, hipStream_t stream
 }
 
 template <int D>
-hipError_t launch_flags(int dtype, bool causal, bool has_mask, const AttnParams& p, int grid,
-                        hipStream_t stream) {
+hipError_t launch_flags(int dtype, bool causal, bool has_mask, AttnParams& p, hipStream_t stream) {
   if (causal) {
-    return has_mask ? launch_d<D, true, true>(dtype, p, grid, stream)
-                    : launch_d<D, true, false>(dtype, p, grid, stream);
+    return has_mask ? launch_d<D, true, true>(dtype, p, stream)
+                    : launch_d<D, true, false>(dtype, p, stream);
   }
-  return has_mask ? launch_d<D, false, true>(dtype, p, grid, stream)
-                  : launch_d<D, false, false>(dtype, p, grid, stream);
+  return has_mask ? launch_d<D, false, true>(dtype, p, stream)
+                  : launch_d<D, false, false>(dtype, p, stream);
 }
 
 }  // namespace
 
 int attention_block_m(int /*dtype*/, int /*D*/) { return kBM; }
 
-hipError_t launch_attention(int dtype, int D, bool causal, bool has_mask, const AttnParams& p,
-                            int grid, hipStream_t stream) {
+hipError_t launch_attention(int dtype, int D, bool causal, bool has_mask, AttnParams& p,
+                            hipStream_t stream) {
   switch (D) {
-    case 8: return launch_flags<8>(dtype, causal, has_mask, p, grid, stream);
-    case 16: return launch_flags<16>(dtype, causal, has_mask, p, grid, stream);
-    case 32: return launch_flags<32>(dtype, causal, has_mask, p, grid, stream);
-    case 64: return launch_flags<64>(dtype, causal, has_mask, p, grid, stream);
-    case 128: return launch_flags<128>(dtype, causal, has_mask, p, grid, stream);
+    case 8: return launch_flags<8>(dtype, causal, has_mask, p, stream);
+    case 16: return launch_flags<16>(dtype, causal, has_mask, p, stream);
+    case 32: return launch_flags<32>(dtype, causal, has_mask, p, stream);
+    case 64: return launch_flags<64>(dtype, causal, has_mask, p, stream);
+    case 128: return launch_flags<128>(dtype, causal, has_mask, p, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -95,6 +95,10 @@ extern "C" ttk_status ttk_attention_fwd(const void* q, const void* k, const void
       }
     }
   }
+  // The kernels keep per-lane K/V offsets of up to 64 rows in 32-bit integers.
+  if (k_strides[1] >= (int64_t{1} << 25) || v_strides[1] >= (int64_t{1} << 25)) {
+    return fail(TTK_EUNSUPPORTED, "attention: k/v sequence stride exceeds %d elements", 1 << 25);
+  }
   if (key_valid != nullptr && (mask_strides[0] < 0 || mask_strides[1] < 0)) {
     return fail(TTK_EINVAL, "attention: mask strides must be non-negative");
   }
@@ -117,10 +121,9 @@ extern "C" ttk_status ttk_attention_fwd(const void* q, const void* k, const void
   p.nq = static_cast<int>(nq);
   p.scale_log2 = scale * 1.4426950408889634f;
   p.xcd_swizzle = (p.BH % 8 == 0) ? 1 : 0;
-  const int grid = static_cast<int>(nq * B * H);
 
   const hipError_t err = ttk::launch_attention(dtype, static_cast<int>(D), causal != 0,
-                                               key_valid != nullptr, p, grid,
+                                               key_valid != nullptr, p,
                                                static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     return fail(TTK_ELAUNCH, "attention: launch failed: %s", hipGetErrorString(err));

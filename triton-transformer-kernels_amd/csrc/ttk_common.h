@@ -69,6 +69,8 @@ struct AttnParams {
   int S, H, BH, nq;
   float scale_log2;  // softmax scale * log2(e)
   int xcd_swizzle;   // 1 when BH % 8 == 0: heads are pinned to XCDs
+  int pair;          // causal: a workgroup runs query tiles nq-1-i and i
+  int units;         // workgroups per (batch, head)
 };
 
 // Launch parameters of the residual + LayerNorm kernels.
@@ -89,8 +91,9 @@ struct LnParams {
 };
 
 // Host-side launchers (defined next to their kernels).  Return a HIP error.
+// launch_attention fills p.pair / p.units and sizes the grid itself.
 hipError_t launch_attention(int dtype, int D, bool causal, bool has_mask,
-                            const AttnParams& p, int grid, hipStream_t stream);
+                            AttnParams& p, hipStream_t stream);
 int attention_block_m(int dtype, int D);
 
 hipError_t launch_residual_layernorm(int dtype, const LnParams& p, bool vector_path,
