@@ -107,8 +107,12 @@ def attention_tflops(batch, seq_len, heads, head_dim, causal, dtype, steps=10, w
     return attention_flops(batch, heads, seq_len, head_dim, causal) / (med * 1e-3) / 1e12, med
 
 
-def layer_norm_gbps(hidden: int, rows: int = 32768, steps: int = 20, warmup: int = 3):
-    """Config 3: rotate input sets so their total exceeds the 256 MB MALL."""
+def layer_norm_gbps(hidden: int, rows: int = 32768, steps: int = 50, warmup: int = 5):
+    """Config 3: rotate input sets so their total exceeds the 256 MB MALL.
+
+    The time per call is the average over `steps` back-to-back launches between
+    two events on the launch stream (a per-launch event pair adds microseconds
+    of its own to a ~20 us kernel)."""
     import torch
 
     from transformer_opt.kernels import fused_residual_layer_norm
@@ -132,9 +136,19 @@ def layer_norm_gbps(hidden: int, rows: int = 32768, steps: int = 20, warmup: int
         fused_residual_layer_norm(x, u, w, b, 1e-5)
 
     with torch.inference_mode():
-        _, ms = time_launches(run, steps, warmup)
-    med = statistics.median(ms)
-    return layer_norm_bytes(rows, hidden) / (med * 1e-3) / 1e9, med, nsets
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        begin = torch.cuda.Event(enable_timing=True)
+        finish = torch.cuda.Event(enable_timing=True)
+        begin.record(stream)
+        for _ in range(steps):
+            run()
+        finish.record(stream)
+        torch.cuda.synchronize()
+    ms = begin.elapsed_time(finish) / steps
+    return layer_norm_bytes(rows, hidden) / (ms * 1e-3) / 1e9, ms, nsets
 
 
 def model_tokens_per_second(dtype_name: str, steps: int = 5, warmup: int = 2):
@@ -199,12 +213,13 @@ def cpu_baseline(time_budget_s: float = 20.0):
     }
 
 
-def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024) -> int:
+def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidden: int = 4096) -> int:
     """Launch one kernel `steps` times (after `warmup`) for a profiler run.
 
     attention:      fp32 causal [8,S,16,64], S = --seq-len (1024: the headline step)
     attention_bf16: bf16 causal [1,16384,32,128] (config 5a)
-    layernorm:      fp32 residual+LN rows=32768 hidden=4096 (config 3), one input set
+    layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
+                    among input sets that together exceed twice the 256 MB MALL
     copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
                     FETCH_SIZE and WRITE_SIZE should each read 262144 KiB per dispatch)
     """
@@ -223,12 +238,19 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024) -> in
         fn = lambda: hip_attention(q, k, v, causal=True, out=out)  # noqa: E731
         work = attention_flops(1, 32, 16384, 128, True)
     elif which == "layernorm":
-        x = torch.randn(32768, 4096, device="cuda")
-        u = torch.randn_like(x)
-        w = torch.rand(4096, device="cuda") + 0.5
-        b = torch.randn(4096, device="cuda") * 0.1
-        fn = lambda: fused_residual_layer_norm(x, u, w, b, 1e-5)  # noqa: E731
-        work = layer_norm_bytes(32768, 4096)
+        rows = 32768
+        nsets = max(1, -(-2 * MALL_BYTES // (rows * hidden * 4 * 4)))
+        sets = [(torch.randn(rows, hidden, device="cuda"), torch.randn(rows, hidden, device="cuda"))
+                for _ in range(nsets)]
+        w = torch.rand(hidden, device="cuda") + 0.5
+        b = torch.randn(hidden, device="cuda") * 0.1
+        calls = iter(range(1 << 62))
+
+        def fn():
+            x, u = sets[next(calls) % nsets]
+            fused_residual_layer_norm(x, u, w, b, 1e-5)
+
+        work = layer_norm_bytes(rows, hidden)
     else:
         src = torch.empty(64 * 1024 * 1024, device="cuda")
         dst = torch.empty_like(src)
@@ -266,14 +288,16 @@ def load_traffic(key: str):
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=50)
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")
+    parser.add_argument("--hidden", type=int, default=4096,
+                        help="hidden size of --profile-only layernorm (rows=32768, fp32)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -295,7 +319,7 @@ def main() -> int:
     dev_name = torch.cuda.get_device_name(0)
     log(f"device {dev_name}; library {_native.library_path()}")
     if args.profile_only:
-        return profile_only(args.profile_only, args.steps, args.warmup, args.seq_len)
+        return profile_only(args.profile_only, args.steps, args.warmup, args.seq_len, args.hidden)
 
     # ---- headline: config 2, fp32 causal attention, S=1024 -----------------
     B, S, H, D = 8, 1024, 16, 64

@@ -82,64 +82,61 @@ __device__ __forceinline__ float round_trip(float v) {
   }
 }
 
-template <typename T, int VPL>
-__global__ __launch_bounds__(kLnThreads) void residual_ln_vec_kernel(LnParams p) {
+// One wavefront handles `64 / lanes_per_row` consecutive rows (one row per
+// lane group).  All loads of the group are straight-line code, issued back
+// to back so they are in flight together: lanes past the last row read the
+// last row instead (in bounds, never stored), and the presence of `u` is a
+// kernel-wide template choice.  gamma/beta come in after the statistics, four
+// vectors at a time, when the x/u registers are free again.
+template <typename T, int VPL, bool HAS_U>
+__device__ __forceinline__ void ln_rows(const LnParams& p) {
   constexpr int VN = Vec<T>::N;
   const int lane = threadIdx.x & 63;
   const int lpr = p.lanes_per_row;
   const int rows_per_wave = 64 / lpr;
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kLnThreads / 64) + (threadIdx.x >> 6);
   const int li = lane & (lpr - 1);
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kLnThreads / 64) + (threadIdx.x >> 6);
   const int64_t row = wave * rows_per_wave + lane / lpr;
+  if (wave * rows_per_wave >= p.rows) return;  // whole wavefront
   const bool active = row < p.rows;
-  const int64_t base = row * p.N;
+  const int64_t lrow = active ? row : p.rows - 1;
+  const int64_t vrow = p.N / VN;  // 16-byte vectors per row
+  const int64_t base = row * vrow;
 
-  const u32x4* __restrict__ xv = reinterpret_cast<const u32x4*>(p.x);
-  const u32x4* __restrict__ uv = reinterpret_cast<const u32x4*>(p.u);
+  const u32x4* __restrict__ xv = reinterpret_cast<const u32x4*>(p.x) + lrow * vrow;
+  const u32x4* __restrict__ uv = HAS_U ? reinterpret_cast<const u32x4*>(p.u) + lrow * vrow : nullptr;
+  const u32x4* __restrict__ wv = reinterpret_cast<const u32x4*>(p.w);
+  const u32x4* __restrict__ bv = reinterpret_cast<const u32x4*>(p.b);
 
-  float r[VPL][VN];
   u32x4 rawx[VPL], rawu[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int64_t vi = base / VN + j * lpr + li;  // 16-byte vector index
-    if (active) {
-      rawx[j] = __builtin_nontemporal_load(xv + vi);
-      if (uv != nullptr) rawu[j] = __builtin_nontemporal_load(uv + vi);
-    } else {
-      rawx[j] = u32x4{0u, 0u, 0u, 0u};
-      rawu[j] = u32x4{0u, 0u, 0u, 0u};
-    }
+    rawx[j] = __builtin_nontemporal_load(xv + j * lpr + li);
+    if constexpr (HAS_U) rawu[j] = __builtin_nontemporal_load(uv + j * lpr + li);
   }
-  bool row_ok = true;
-  if (p.valid != nullptr && active) row_ok = p.valid[row] != 0;
+  const bool row_ok = p.valid == nullptr || p.valid[lrow] != 0;
   const bool zero_r = p.zero_res && !row_ok;
 
+  float r[VPL][VN];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     float xf[VN];
     unpack(T{}, rawx[j], xf);
-    if (uv != nullptr) {
+    if constexpr (HAS_U) {
       float uf[VN];
       unpack(T{}, rawu[j], uf);
 #pragma unroll
-      for (int i = 0; i < VN; ++i) r[j][i] = round_trip<T>(xf[i] + uf[i]);
+      for (int i = 0; i < VN; ++i) r[j][i] = zero_r ? 0.0f : round_trip<T>(xf[i] + uf[i]);
     } else {
 #pragma unroll
-      for (int i = 0; i < VN; ++i) r[j][i] = xf[i];
-    }
-    if (zero_r) {
-#pragma unroll
-      for (int i = 0; i < VN; ++i) r[j][i] = 0.0f;
+      for (int i = 0; i < VN; ++i) r[j][i] = zero_r ? 0.0f : xf[i];
     }
   }
 
   if (p.r_out != nullptr && active) {
-    u32x4* __restrict__ ro = reinterpret_cast<u32x4*>(p.r_out);
+    u32x4* __restrict__ ro = reinterpret_cast<u32x4*>(p.r_out) + base;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int64_t vi = base / VN + j * lpr + li;
-      __builtin_nontemporal_store(pack(T{}, r[j]), ro + vi);
-    }
+    for (int j = 0; j < VPL; ++j) __builtin_nontemporal_store(pack(T{}, r[j]), ro + j * lpr + li);
   }
 
   // Per-lane exact statistics of VPL*VN values.
@@ -173,27 +170,42 @@ __global__ __launch_bounds__(kLnThreads) void residual_ln_vec_kernel(LnParams p)
   const bool zero_y = p.zero_norm && !row_ok;
 
   if (!active) return;
-  const u32x4* __restrict__ wv = reinterpret_cast<const u32x4*>(p.w);
-  const u32x4* __restrict__ bv = reinterpret_cast<const u32x4*>(p.b);
-  u32x4* __restrict__ yo = reinterpret_cast<u32x4*>(p.y_out);
+  u32x4* __restrict__ yo = reinterpret_cast<u32x4*>(p.y_out) + base;
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int cv = j * lpr + li;  // vector index inside the row
-    float wf[VN], bf[VN];
-    unpack(T{}, wv[cv], wf);
-    if (bv != nullptr) {
-      unpack(T{}, bv[cv], bf);
-    } else {
+  for (int j0 = 0; j0 < VPL; j0 += 4) {
+    u32x4 cw[4], cb[4];
 #pragma unroll
-      for (int i = 0; i < VN; ++i) bf[i] = 0.0f;
+    for (int jj = 0; jj < 4; ++jj) {
+      if (j0 + jj < VPL) {
+        cw[jj] = wv[(j0 + jj) * lpr + li];
+        cb[jj] = bv != nullptr ? bv[(j0 + jj) * lpr + li] : u32x4{0u, 0u, 0u, 0u};
+      }
     }
-    float y[VN];
 #pragma unroll
-    for (int i = 0; i < VN; ++i) {
-      const float n = (r[j][i] - mean) * rstd;
-      y[i] = zero_y ? 0.0f : __builtin_fmaf(n, wf[i], bf[i]);
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = j0 + jj;
+      if (j < VPL) {
+        float wf[VN], bf[VN], y[VN];
+        unpack(T{}, cw[jj], wf);
+        unpack(T{}, cb[jj], bf);
+#pragma unroll
+        for (int i = 0; i < VN; ++i) {
+          const float n = (r[j][i] - mean) * rstd;
+          y[i] = zero_y ? 0.0f : __builtin_fmaf(n, wf[i], bf[i]);
+        }
+        __builtin_nontemporal_store(pack(T{}, y), yo + j * lpr + li);
+      }
     }
-    __builtin_nontemporal_store(pack(T{}, y), yo + base / VN + cv);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <typename T, int VPL>
+__global__ __launch_bounds__(kLnThreads) void residual_ln_vec_kernel(LnParams p) {
+  if (p.u != nullptr) {
+    ln_rows<T, VPL, true>(p);
+  } else {
+    ln_rows<T, VPL, false>(p);
   }
 }
 
