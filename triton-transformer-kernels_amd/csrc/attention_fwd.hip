@@ -486,20 +486,35 @@ struct H16Cfg {
   static constexpr int KS = DK + 8;                  // LDS K row stride (elements, 16-byte pad)
   static constexpr int NDB = (D + 31) / 32;          // output blocks of 32 d-rows
   static constexpr int G = DK / 16;                  // Q.K k-steps of 16
-  static constexpr int VTS = BN + 4;                 // V^T row stride (elements)
-  // V^T store: a thread moves 4 keys x 8 d (four 16-byte global loads).
-  static constexpr int VGROUPS = (BN / 4) * CPR;
-  static constexpr int VPT = (VGROUPS + kThreads - 1) / kThreads;
+  // LDS V row stride (elements): row-major V tile whose stride is 16 dwords
+  // mod 64 banks, so the 4 key rows one half-wave reads with the transposing
+  // load fall on disjoint banks.
+  static constexpr int VS = D == 128 ? 160 : D == 64 ? 96 : D;
+  static constexpr int VCH = VS / 8;                 // 16-byte chunks per LDS V row
+  // Head dims below 32 read up to d = 31 with the transposing load (rows
+  // d >= D of the result are never stored); the slack keeps those reads of
+  // the last rows inside the buffer.
+  static constexpr int VSLACK = 32;
   static constexpr int NSTEP = NSB * 2 * NDB;        // P.V MFMAs per tile
 };
+
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes,
+// lane 4a+c receives element c of the 8-byte rows addressed by lanes a, a+4,
+// a+8 and a+12 of the group (in that order).
+__device__ __forceinline__ u16x4 lds_read_tr16(const unsigned short* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u16x4, v);
+}
 
 template <typename T, int D, bool CAUSAL, bool HAS_MASK>
 __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_kernel(AttnParams p) {
   using C = H16Cfg<D>;
   constexpr int BN = C::BN, NSB = C::NSB, CPR = C::CPR, KS = C::KS,
-                NDB = C::NDB, VTS = C::VTS, VPT = C::VPT, G = C::G, NSTEP = C::NSTEP;
+                NDB = C::NDB, VS = C::VS, VCH = C::VCH, G = C::G, NSTEP = C::NSTEP;
   __shared__ __attribute__((aligned(16))) unsigned short smK[2][BN * KS];
-  __shared__ __attribute__((aligned(16))) unsigned short smVt[2][D * VTS];
+  __shared__ __attribute__((aligned(16))) unsigned short smV[2][BN * VS + C::VSLACK];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -543,6 +558,23 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     const int cc = pos - row * KCH;
     koff[i] = pos < BN * KCH ? row * static_cast<int>(p.ks) + 8 * (cc < CPR ? cc : 0) : -1;
   }
+  // V: LDS-DMA into row-major rows of VCH 16-byte chunks (read back with the
+  // transposing load); pad chunks copy a data chunk of the same row again.
+  constexpr int NV = (BN * VCH + 63) / 64;
+  constexpr int VPW = (NV + NW - 1) / NW;
+  int voff[VPW];
+#pragma unroll
+  for (int i = 0; i < VPW; ++i) {
+    const int pos = 64 * (wave + NW * i) + lane;
+    const int row = pos / VCH;
+    const int cc = pos - row * VCH;
+    voff[i] = pos < BN * VCH ? row * static_cast<int>(p.vs) + 8 * (cc < CPR ? cc : cc - CPR) : -1;
+  }
+  // Per-lane base of the transposing V reads: lane i of 16-lane group g
+  // addresses key row 4*(g/2) + i/4 and d = 16*(g%2) + 4*(i%4), so lane
+  // (m, h) receives V[4h + 0..3][m] (see lds_read_tr16); P.V step (kstep,
+  // db) adds 16*kstep rows and 32*db columns, its upper four keys 8 rows.
+  const int vbase = (4 * h + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   {
     // 16-bit workgroups run one query tile (never paired: a second pass costs
@@ -567,7 +599,6 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     const int kv_end = CAUSAL ? min(S, (qb + 1) * kBM) : S;
     const int ntiles = (kv_end + BN - 1) / BN;
 
-    u32x4 rv[VPT][4];
     bool rm = false;
     auto dma_k = [&](int buf, int t) __attribute__((always_inline)) {
       if constexpr (HAS_MASK) {
@@ -601,40 +632,21 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         return range_bits(t * BN, S);
       }
     };
-    // V: VPT groups of 4 keys x 8 d per thread, staged in registers and
-    // transposed on the LDS store; keys past S read as zeros.
-    auto gload_v = [&](int t) __attribute__((always_inline)) {
+    auto dma_v = [&](int buf, int t) __attribute__((always_inline)) {
+      const St* vt = V + static_cast<int64_t>(t) * BN * p.vs;
+      const bool ragged = (t + 1) * BN > S;
 #pragma unroll
-      for (int i = 0; i < VPT; ++i) {
-        const int gi = tid + kThreads * i;
-        if (C::VGROUPS % kThreads == 0 || gi < C::VGROUPS) {
-          const int kq = gi / CPR;  // key quad
-          const int cc = gi - kq * CPR;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int key = t * BN + 4 * kq + e;
-            rv[i][e] = key < S ? *reinterpret_cast<const u32x4*>(V + key * p.vs + 8 * cc)
-                               : u32x4{0u, 0u, 0u, 0u};
-          }
-        }
-      }
-    };
-    auto lstore_v = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-      for (int i = 0; i < VPT; ++i) {
-        const int gi = tid + kThreads * i;
-        if (C::VGROUPS % kThreads == 0 || gi < C::VGROUPS) {
-          const int kq = gi / CPR;
-          const int cc = gi - kq * CPR;
-          // Transpose 4 keys x 8 d into 8 rows of V^T (4 consecutive keys each).
-#pragma unroll
-          for (int dd = 0; dd < 8; ++dd) {
-            const int word = dd >> 1;
-            const int shift = (dd & 1) * 16;
-            u32x2 packed;
-            packed[0] = ((rv[i][0][word] >> shift) & 0xffffu) | (((rv[i][1][word] >> shift) & 0xffffu) << 16);
-            packed[1] = ((rv[i][2][word] >> shift) & 0xffffu) | (((rv[i][3][word] >> shift) & 0xffffu) << 16);
-            *reinterpret_cast<u32x2*>(&smVt[buf][(8 * cc + dd) * VTS + 4 * kq]) = packed;
+      for (int i = 0; i < VPW; ++i) {
+        const int j = wave + NW * i;
+        if (j < NV && voff[i] >= 0) {
+          if (!ragged) {
+            dma16(vt + voff[i], &smV[buf][512 * j]);
+          } else {
+            const int pos = 64 * j + lane;
+            const int row = pos / VCH;
+            const int cc = pos - row * VCH;
+            const int key = min(t * BN + row, S - 1);
+            dma16(V + key * p.vs + 8 * (cc < CPR ? cc : cc - CPR), &smV[buf][512 * j]);
           }
         }
       }
@@ -645,15 +657,15 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       return *reinterpret_cast<const u16x8*>(&smK[buf][row * KS + 16 * g + 8 * h]);
     };
     // A operand of P.V step idx = ((sb * 2 + j) * NDB + db): d-row 32*db + m,
-    // keys sb*32 + 16j + 4h + {0..3} and sb*32 + 16j + 8 + 4h + {0..3}.
+    // keys sb*32 + 16j + 4h + {0..3} and sb*32 + 16j + 8 + 4h + {0..3}.  For
+    // head dims below 32 the rows d >= D hold other data; they only reach
+    // output rows that are never stored.
     auto vread = [&](int buf, int idx) __attribute__((always_inline)) -> u16x8 {
       const int db = idx % NDB;
       const int kstep = idx / NDB;  // sb * 2 + j
-      const int d = 32 * db + m;
-      if (D < 32 && d >= D) return u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      const int kbase = 16 * kstep + 4 * h;
-      const u16x4 lo = *reinterpret_cast<const u16x4*>(&smVt[buf][d * VTS + kbase]);
-      const u16x4 hi = *reinterpret_cast<const u16x4*>(&smVt[buf][d * VTS + kbase + 8]);
+      const unsigned short* base = &smV[buf][vbase + 16 * kstep * VS + 32 * db];
+      const u16x4 lo = lds_read_tr16(base);
+      const u16x4 hi = lds_read_tr16(base + 8 * VS);
       return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
@@ -801,8 +813,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     bool pending = false;  // a tile's P.V is still to be accumulated (uniform)
     int pend_live = 0;     // its number of live sub-blocks
 
-    auto finish_tile = [&](int t, int kb) __attribute__((always_inline)) {
-      lstore_v(kb);
+    auto finish_tile = [&](int t) __attribute__((always_inline)) {
       vm_wait();
       const uint64_t kvalid_next = key_bits(t + 1);
       __syncthreads();
@@ -813,7 +824,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       // K(t+1) goes to the buffer K(t-1) used, V(t) to the one V(t-2) used;
       // neither is read in this iteration.
       if (t + 1 < ntiles) dma_k(kb ^ 1, t + 1);
-      gload_v(t);
+      dma_v(kb, t);
       const int k0 = t * BN;
       const bool live = q0 < S && (!CAUSAL || k0 <= q0 + 31);
       int nlive = NSB;
@@ -834,14 +845,14 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         pend_live = nlive;
       }
       pending = live;
-      finish_tile(t, kb);
+      finish_tile(t);
     };
 
     generic_tile(0);
     for (int t = 1; t < n_full; ++t) {
       const int kb = t & 1;
       if (t + 1 < ntiles) dma_k(kb ^ 1, t + 1);
-      gload_v(t);
+      dma_v(kb, t);
       f32x16 s[NSB];
       u16x8 pn[NSB * 2];
       qk(std::false_type{}, kb, NSB, s);
@@ -853,7 +864,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       }
 #pragma unroll
       for (int i = 0; i < NSB * 2; ++i) pk[i] = pn[i];
-      finish_tile(t, kb);
+      finish_tile(t);
     }
     for (int t = max(1, n_full); t < ntiles; ++t) generic_tile(t);
     if (pending) pv((ntiles - 1) & 1, pend_live);
