@@ -218,6 +218,7 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
 
     attention:      fp32 causal [8,S,16,64], S = --seq-len (1024: the headline step)
     attention_bf16: bf16 causal [1,16384,32,128] (config 5a)
+    attention_bf16_d64: bf16 causal [4,2048,16,64] (the attention of the config-4 encoder)
     layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
                     among input sets that together exceed twice the 256 MB MALL
     copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
@@ -237,6 +238,11 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         out = torch.empty_like(q)
         fn = lambda: hip_attention(q, k, v, causal=True, out=out)  # noqa: E731
         work = attention_flops(1, 32, 16384, 128, True)
+    elif which == "attention_bf16_d64":
+        q, k, v = make_qkv(4, 2048, 16, 64, torch.bfloat16, seed=6)
+        out = torch.empty_like(q)
+        fn = lambda: hip_attention(q, k, v, causal=True, out=out)  # noqa: E731
+        work = attention_flops(4, 16, 2048, 64, True)
     elif which == "layernorm":
         rows = 32768
         nsets = max(1, -(-2 * MALL_BYTES // (rows * hidden * 4 * 4)))
@@ -292,7 +298,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=50)
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16"),
+    parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16",
+                                                   "attention_bf16_d64"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")
