@@ -219,6 +219,8 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
     attention:      fp32 causal [8,S,16,64], S = --seq-len (1024: the headline step)
     attention_bf16: bf16 causal [1,16384,32,128] (config 5a)
     attention_bf16_d64: bf16 causal [4,2048,16,64] (the attention of the config-4 encoder)
+    encoder_fp32 / encoder_bf16: config-4 encoder forward (hipGraph replay), for the
+                    per-kernel split
     layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
                     among input sets that together exceed twice the 256 MB MALL
     copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
@@ -257,6 +259,16 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
             fused_residual_layer_norm(x, u, w, b, 1e-5)
 
         work = layer_norm_bytes(rows, hidden)
+    elif which in ("encoder_fp32", "encoder_bf16"):
+        from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
+
+        dtype = torch.float32 if which == "encoder_fp32" else torch.bfloat16
+        torch.manual_seed(1234)
+        model = UserOptimizedTransformer(TransformerConfig(4, 2048, 1024, 16, 4096, 6, True))
+        model = model.to(device="cuda", dtype=dtype).eval()
+        x = torch.randn(4, 2048, 1024, device="cuda").to(dtype)
+        fn = lambda: model(x)  # noqa: E731
+        work = 4 * 2048  # tokens
     else:
         src = torch.empty(64 * 1024 * 1024, device="cuda")
         dst = torch.empty_like(src)
@@ -274,8 +286,12 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         finish.record()
         torch.cuda.synchronize()
     ms = begin.elapsed_time(finish) / steps
-    rate = work / (ms * 1e-3) / (1e9 if which in ("layernorm", "copy") else 1e12)
-    unit = "GB/s" if which in ("layernorm", "copy") else "TFLOP/s"
+    if which in ("layernorm", "copy"):
+        rate, unit = work / (ms * 1e-3) / 1e9, "GB/s"
+    elif which.startswith("encoder"):
+        rate, unit = work / (ms * 1e-3), "tokens/s"
+    else:
+        rate, unit = work / (ms * 1e-3) / 1e12, "TFLOP/s"
     print(json.dumps({"profile_only": which, "steps": steps, "avg_launch_us": round(ms * 1e3, 2),
                       "rate": round(rate, 2), "unit": unit}), flush=True)
     return 0
@@ -299,7 +315,7 @@ def main() -> int:
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16",
-                                                   "attention_bf16_d64"),
+                                                   "attention_bf16_d64", "encoder_fp32", "encoder_bf16"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")

@@ -288,3 +288,36 @@ def test_determinism_bitwise(gpu_ready):
     a = run_hip(q, k, v, None, True)
     b = run_hip(q, k, v, None, True)
     assert torch.equal(a, b)
+
+
+def test_config5a_long_sequence_bf16_rows_and_memory(gpu_ready):
+    # BASELINE config 5a: causal bf16, B=1, H=32, S=16384, D=128, run at full
+    # size.  Query rows are independent, so the chunked oracle on sampled
+    # (head, row-block) pairs - start, middle and end of the sequence, where
+    # the rows meet 128 to 16384 keys - checks those rows of the full run.
+    # Memory: the kernel keeps no workspace, so with a caller-owned output a
+    # launch allocates nothing at all.
+    from transformer_opt.kernels import hip_attention
+
+    batch, seq_len, heads, head_dim = 1, 16384, 32, 128
+    g = torch.Generator().manual_seed(37)
+    q, k, v = (torch.randn(batch, seq_len, heads, head_dim, generator=g).to(torch.bfloat16)
+               for _ in range(3))
+    dev = torch.device("cuda")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = torch.empty_like(qd)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    before = torch.cuda.memory_allocated()
+    with torch.inference_mode():
+        hip_attention(qd, kd, vd, causal=True, out=out)
+    torch.cuda.synchronize()
+    assert torch.cuda.max_memory_allocated() == before
+    result = out.cpu()
+    assert torch.isfinite(result).all()
+    pairs = [(0, 0), (0, 17), (0, 31)]
+    qf, kf, vf = q.float(), k.float(), v.float()
+    for rows in (slice(0, 128), slice(8128, 8256), slice(16256, 16384)):
+        reference = chunked_kernel_contract_attention(qf, kf, vf, None, True, heads=pairs, query_rows=rows)
+        actual = torch.stack([result[b, rows, h, :] for b, h in pairs])
+        assert contract_failures(actual, reference) == 0, f"rows {rows}"
