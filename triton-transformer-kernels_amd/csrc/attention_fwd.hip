@@ -32,9 +32,9 @@
 //       which does not issue alongside MFMA) as the bound, so the loop is
 //       software-pipelined: iteration t computes S(t) = K(t).Q^T and then one
 //       instruction stream interleaving the P.V MFMAs of tile t-1 with the
-//       softmax of tile t.  K(t+1) is copied global->LDS by LDS-DMA
-//       (global_load_lds_dwordx4, no register staging); V(t) is staged in
-//       registers and stored transposed.
+//       softmax of tile t.  K(t+1) and V(t) are copied global->LDS by LDS-DMA
+//       (global_load_lds_dwordx4, no register staging); V stays row-major and
+//       the P.V operand is read with the transposing ds_read_b64_tr_b16.
 // * Masking: key validity (key mask and key < S) is a wave-uniform 64-bit
 //   ballot per tile; with the lane's causal limit it becomes one bit mask per
 //   32-key sub-block.  Only tiles that need it (diagonal, ragged end, key
@@ -55,8 +55,8 @@
 // domain.  bf16/fp16 path: v_mfma_f32_32x32x16_{bf16,f16}; scores stay fp32,
 // the row max is taken on raw scores and the scale is folded into one fma per
 // element before exp2; P is rounded to the input type (v_cvt_pk_bf16_f32 /
-// v_cvt_f16_f32) for the P.V product; V is stored transposed in LDS so the
-// 16-bit A operand (8 keys of one d) is two 8-byte LDS reads.
+// v_cvt_f16_f32) for the P.V product; the 16-bit A operand (8 keys of one d)
+// is two transposing 8-byte LDS reads of the row-major V tile.
 #include <atomic>
 
 #include "ttk_common.h"
