@@ -60,6 +60,14 @@ CASES = [
     (3, 100, 2, 32, torch.float32, True, "prefix", 1.0),
     (3, 100, 2, 64, torch.bfloat16, True, "prefix", 1.0),
     (2, 140, 2, 128, torch.bfloat16, False, "prefix", 1.0),
+    # Longer fp32 rows with key masks (several full tiles before the masked
+    # diagonal and ragged tiles) and a sequence shorter than one query tile.
+    (2, 512, 2, 64, torch.float32, True, "prefix", 1.0),
+    (2, 513, 2, 64, torch.float32, True, "prefix", 1.0),
+    (2, 700, 2, 64, torch.float32, True, "prefix", 1.0),
+    (1, 777, 3, 32, torch.float32, False, "prefix", 1.0),
+    (2, 640, 2, 16, torch.float32, True, "prefix", 1.0),
+    (3, 64, 4, 64, torch.float32, False, "prefix", 1.0),
 ]
 
 
