@@ -496,6 +496,9 @@ struct H16Cfg {
   // the last rows inside the buffer.
   static constexpr int VSLACK = 32;
   static constexpr int NSTEP = NSB * 2 * NDB;        // P.V MFMAs per tile
+  // Operand prefetch distances (ring depths) of the K and V fragments.
+  static constexpr int PDK = 2;
+  static constexpr int PDV = 2;
 };
 
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes,
@@ -512,7 +515,8 @@ template <typename T, int D, bool CAUSAL, bool HAS_MASK>
 __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_kernel(AttnParams p) {
   using C = H16Cfg<D>;
   constexpr int BN = C::BN, NSB = C::NSB, CPR = C::CPR, KS = C::KS,
-                NDB = C::NDB, VS = C::VS, VCH = C::VCH, G = C::G, NSTEP = C::NSTEP;
+                NDB = C::NDB, VS = C::VS, VCH = C::VCH, G = C::G, NSTEP = C::NSTEP,
+                PDK = C::PDK, PDV = C::PDV;
   __shared__ __attribute__((aligned(16))) unsigned short smK[2][BN * KS];
   __shared__ __attribute__((aligned(16))) unsigned short smV[2][BN * VS + C::VSLACK];
 
@@ -681,45 +685,47 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
 #pragma unroll
     for (int i = 0; i < NSB * 2; ++i) pk[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
 
+    // S^T = K(buf) . Q^T.  K fragments run PDK groups ahead in a ring: the
+    // slot of group g is refilled with group g + PDK right after group g's
+    // MFMAs issue, so an LDS read has PDK - 1 groups of MFMAs to land.
     auto qk = [&](auto masked_tag, int buf, int nlive, f32x16 (&s)[NSB]) {
       constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
-      u16x8 kf[NSB];
+      u16x8 kr[PDK][NSB];
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
-        if (!MASKED || sb < nlive) kf[sb] = kread(buf, sb, 0);
+      for (int i = 0; i < PDK && i < G; ++i)
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb)
+          if (!MASKED || sb < nlive) kr[i][sb] = kread(buf, sb, i);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        u16x8 kn[NSB];
-        if (g + 1 < G) {
-#pragma unroll
-          for (int sb = 0; sb < NSB; ++sb)
-            if (!MASKED || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
-        }
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb) {
           if (MASKED && sb >= nlive) continue;
-          s[sb] = mfma_16(T{}, kf[sb], qf[g], s[sb]);
+          s[sb] = mfma_16(T{}, kr[g % PDK][sb], qf[g], s[sb]);
         }
-        if (g + 1 < G) {
+        if (g + PDK < G) {
 #pragma unroll
-          for (int sb = 0; sb < NSB; ++sb) kf[sb] = kn[sb];
+          for (int sb = 0; sb < NSB; ++sb)
+            if (!MASKED || sb < nlive) kr[g % PDK][sb] = kread(buf, sb, g + PDK);
         }
         fence();
       }
     };
 
+    // O^T += V^T(buf) . P^T; V fragments run PDV steps ahead in a ring.
     auto pv = [&](int buf, int nlive) __attribute__((always_inline)) {
       const int nsteps = nlive * 2 * NDB;
-      u16x8 vf = vread(buf, 0);
+      u16x8 vr[PDV];
+#pragma unroll
+      for (int i = 0; i < PDV && i < NSTEP; ++i)
+        if (i < nsteps) vr[i] = vread(buf, i);
 #pragma unroll
       for (int idx = 0; idx < NSTEP; ++idx) {
         if (idx < nsteps) {
-          u16x8 vn{};
-          if (idx + 1 < NSTEP && idx + 1 < nsteps) vn = vread(buf, idx + 1);
-          acc[idx % NDB] = mfma_16(T{}, vf, pk[idx / NDB], acc[idx % NDB]);
-          vf = vn;
+          acc[idx % NDB] = mfma_16(T{}, vr[idx % PDV], pk[idx / NDB], acc[idx % NDB]);
+          if (idx + PDV < NSTEP && idx + PDV < nsteps) vr[idx % PDV] = vread(buf, idx + PDV);
         }
         fence();
       }
@@ -762,12 +768,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       constexpr int PER = E / HALF;    // elements per step in each phase
       float mt = -INFINITY;
       float ls = 0.0f, m_new = 0.0f, m_use = 0.0f, alpha = 0.0f, mc = 0.0f;
-      u16x8 vf = vread(buf, 0);
+      u16x8 vr[PDV];
+#pragma unroll
+      for (int i = 0; i < PDV && i < NSTEP; ++i) vr[i] = vread(buf, i);
 #pragma unroll
       for (int idx = 0; idx < NSTEP; ++idx) {
-        u16x8 vn{};
-        if (idx + 1 < NSTEP) vn = vread(buf, idx + 1);
-        acc[idx % NDB] = mfma_16(T{}, vf, pk[idx / NDB], acc[idx % NDB]);
+        acc[idx % NDB] = mfma_16(T{}, vr[idx % PDV], pk[idx / NDB], acc[idx % NDB]);
+        if (idx + PDV < NSTEP) vr[idx % PDV] = vread(buf, idx + PDV);
         if (idx < HALF) {
 #pragma unroll
           for (int j = 0; j < PER; ++j) {
@@ -790,7 +797,6 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
             pn[(e >> 4) * 2 + ((e & 15) >> 3)][e & 7] = to_bits(T{}, pr);
           }
         }
-        vf = vn;
         fence();
       }
       l_run = __builtin_fmaf(l_run, alpha, ls);
