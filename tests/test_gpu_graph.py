@@ -178,3 +178,36 @@ def test_other_shapes_and_dtypes_replay_bitwise(gpu_ready):
                 torch.cuda.synchronize()
                 assert torch.equal(out, eager(x)), (dtype, step)
         assert model.cuda_graph_replays == 3
+
+
+def test_alternating_shapes_replay_without_recapture_and_evict_lru(gpu_ready):
+    # Up to max_cuda_graphs captures live side by side, one per input geometry;
+    # the least recently used is evicted; a parameter change drops them all.
+    model = make_model(max_cuda_graphs=2).cuda()
+    eager = make_model(execution_mode="eager").cuda()
+    eager.load_state_dict(model.state_dict(), strict=True)
+    shapes = [(1, 64, 128), (2, 48, 128), (3, 32, 128)]
+    with torch.inference_mode():
+        xs = [torch.randn(shape, device="cuda") for shape in shapes]
+        model(xs[0])
+        first = model._inference_graph
+        model(xs[1])
+        second = model._inference_graph
+        assert second is not first
+        for _ in range(2):
+            out0 = model(xs[0])
+            assert model._inference_graph is first
+            out1 = model(xs[1])
+            assert model._inference_graph is second
+        assert torch.equal(out0, eager(xs[0])) and torch.equal(out1, eager(xs[1]))
+        model(xs[2])  # evicts the least recently used capture (shape 0)
+        assert len(model._inference_graphs) == 2
+        model(xs[0])
+        assert model._inference_graph is not first
+        assert model.cuda_graph_replays == 8
+        with torch.no_grad():
+            model.layers[0].ffn_in.bias.add_(0.01)
+        model(xs[1])
+        assert len(model._inference_graphs) == 1 and model._inference_graph is not second
+    with pytest.raises(ValueError, match="max_cuda_graphs"):
+        make_model(max_cuda_graphs=0)

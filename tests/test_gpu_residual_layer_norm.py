@@ -81,7 +81,7 @@ def test_widths_vector_and_fallback_paths(gpu_ready, hidden):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("hidden", [128, 1024, 1000])
+@pytest.mark.parametrize("hidden", [32, 64, 128, 1024, 1000])
 def test_low_precision_rows(gpu_ready, dtype, hidden):
     g = torch.Generator().manual_seed(99)
     x = torch.randn(50, hidden, generator=g).to(dtype)

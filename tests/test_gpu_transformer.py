@@ -111,6 +111,29 @@ def test_bf16_model_within_stated_bound(gpu_ready, causal):
     assert err.mean().item() <= 1e-2
 
 
+@pytest.mark.parametrize("padding", [0.0, 0.3])
+def test_fp16_model_within_stated_bound(gpu_ready, padding):
+    # fp16 end to end (the reference's other supported dtype, config.py:17-18),
+    # with and without key padding; fp32 oracle on the fp16-rounded weights and
+    # input.  fp16 keeps 11 significant bits, so the bf16 bound (8 bits) holds
+    # with margin; rows the mask invalidates must be exact zeros.
+    cfg = TransformerConfig(2, 160, 512, 8, 2048, 3, True)
+    baseline, model = build(cfg, dtype=torch.float16)
+    baseline.load_state_dict({k: v.to(torch.float16).float() for k, v in baseline.state_dict().items()})
+    x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 9, padding, 1.0)
+    x = x.to(torch.float16)
+    with torch.inference_mode():
+        ref = baseline(x.float(), mask)
+        out = model(x.cuda(), None if mask is None else mask.cuda())
+    assert out.dtype == torch.float16
+    err = (out.float().cpu() - ref).abs()
+    ok = (err <= 5e-2) | (err <= 0.05 * ref.abs())
+    assert bool(ok.all()), f"failed={int((~ok).sum())} max_abs={err.max().item():.3g}"
+    assert err.mean().item() <= 1e-2
+    if mask is not None:
+        assert bool((out.float().cpu()[~mask] == 0).all())
+
+
 def test_explicit_all_valid_mask_matches_no_mask(gpu_ready):
     cfg = TransformerConfig(2, 33, 64, 4, 128, 1, True)
     _, model = build(cfg, execution_mode="eager")

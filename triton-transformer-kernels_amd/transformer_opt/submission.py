@@ -7,7 +7,7 @@
 ``cuda_graph_replays``, ``reset_attention_backend_counts()``,
 ``clear_cuda_graph()``, ``_can_replay_cuda_graph()``, a state-dict key set
 identical to the organizer baseline, a non-persistent packed-QKV projection
-cache invalidated by parameter versions, and bounded single-graph replay.
+cache invalidated by parameter versions, and bounded graph replay.
 
 What is MI355X-specific:
 
@@ -21,7 +21,9 @@ What is MI355X-specific:
   (submission.py:184-190 restricted it to measured widths);
 * graph replay (torch.cuda.CUDAGraph, i.e. a hipGraph on ROCm) is eligible for
   every supported shape and dtype instead of an exact measured shape set
-  (submission.py:582-590).
+  (submission.py:582-590), and up to ``max_cuda_graphs`` captures (one per
+  input geometry: shape, dtype, mask presence, inference mode) are kept, so a
+  caller alternating between shapes replays instead of recapturing.
 
 Projections and the FFN stay library GEMMs (hipBLASLt through F.linear).
 The model is forward-inference only: a call with gradients enabled on
@@ -31,6 +33,7 @@ parameters that require them raises, as there is no backward kernel.
 from __future__ import annotations
 
 import threading
+from collections import OrderedDict
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -50,8 +53,11 @@ _EXECUTION_MODES = ("auto", "eager")
 class UserOptimizedTransformer(nn.Module):
     """Pre-LN encoder whose attention and LayerNorms run on gfx950 HIP kernels."""
 
-    def __init__(self, config, attention_backend: str = "auto", execution_mode: str = "auto") -> None:
+    def __init__(self, config, attention_backend: str = "auto", execution_mode: str = "auto",
+                 max_cuda_graphs: int = 4) -> None:
         super().__init__()
+        if not isinstance(max_cuda_graphs, int) or max_cuda_graphs < 1:
+            raise ValueError("max_cuda_graphs must be a positive integer")
         if attention_backend not in ATTENTION_BACKENDS:
             raise ValueError(
                 f"attention_backend must be one of {ATTENTION_BACKENDS}, got {attention_backend!r}"
@@ -66,7 +72,12 @@ class UserOptimizedTransformer(nn.Module):
         self.final_norm = nn.LayerNorm(config.d_model)
         self.attention_backend = attention_backend
         self.execution_mode = execution_mode
-        self._inference_graph = None
+        # Captured forwards keyed by input geometry, least recently used first;
+        # all of them belong to one model state (``_graph_model_key``).
+        self.max_cuda_graphs = max_cuda_graphs
+        self._inference_graphs: "OrderedDict[tuple, _InferenceGraph]" = OrderedDict()
+        self._graph_model_key = None
+        self._inference_graph = None  # the entry used last
         self._inference_graph_lock = threading.RLock()
         self.cuda_graph_replays = 0
         self.attention_backend_counts: Dict[str, int] = {"hip": 0}
@@ -84,6 +95,8 @@ class UserOptimizedTransformer(nn.Module):
     def __getstate__(self):
         state = super().__getstate__().copy()
         state["_inference_graph"] = None
+        state["_inference_graphs"] = OrderedDict()
+        state["_graph_model_key"] = None
         state.pop("_inference_graph_lock", None)
         return state
 
@@ -180,11 +193,21 @@ class UserOptimizedTransformer(nn.Module):
             with self._inference_graph_lock:
                 signature = self._graph_signature(x, valid_token_mask)
                 if signature is not None:
-                    entry = self._inference_graph
-                    if entry is None or entry.signature != signature:
-                        self._inference_graph = None
+                    model_key, geometry = signature
+                    if model_key != self._graph_model_key:
+                        # Parameters, modules or attention settings changed:
+                        # every capture is stale (and would pin old storage).
+                        self._drop_graphs()
+                        self._graph_model_key = model_key
+                    entry = self._inference_graphs.get(geometry)
+                    if entry is None:
                         entry = _InferenceGraph(self, x, valid_token_mask, signature)
-                        self._inference_graph = entry
+                        self._inference_graphs[geometry] = entry
+                        while len(self._inference_graphs) > self.max_cuda_graphs:
+                            self._inference_graphs.popitem(last=False)
+                    else:
+                        self._inference_graphs.move_to_end(geometry)
+                    self._inference_graph = entry
                     output = entry.replay(x, valid_token_mask)
                     for backend, count in entry.backend_counts.items():
                         self.attention_backend_counts[backend] += count
@@ -234,10 +257,12 @@ class UserOptimizedTransformer(nn.Module):
         return True
 
     def _graph_signature(self, x, valid_token_mask):
-        """Everything a captured graph bakes in (reference submission.py:603-641):
-        parameter storage/version/device/dtype, module eps and shapes, hooks,
-        training flags, attention config, input geometry, mask presence and
-        the inference-mode context.  None means "do not capture"."""
+        """Everything a captured graph bakes in (reference submission.py:603-641),
+        as ``(model_key, geometry)``: the model key holds parameter
+        storage/version/device/dtype, module eps and shapes, hooks, training
+        flags and the attention config; the geometry holds the input's device,
+        shape and dtype, mask presence and the inference-mode context.  None
+        means "do not capture"."""
         stack = [self]
         seen_modules, seen_parameters = set(), set()
         modules, parameters = [], []
@@ -266,16 +291,21 @@ class UserOptimizedTransformer(nn.Module):
              layer.attention.head_dim, layer.attention.scale)
             for layer in self.layers
         )
-        return (
-            tuple(parameters), tuple(modules), attention_config, self.config, self.attention_backend,
-            x.device, tuple(x.shape), x.dtype, valid_token_mask is not None,
-            torch.backends.cuda.matmul.allow_tf32, torch.is_inference_mode_enabled(),
-        )
+        model_key = (tuple(parameters), tuple(modules), attention_config, self.config,
+                     self.attention_backend, torch.backends.cuda.matmul.allow_tf32)
+        geometry = (x.device, tuple(x.shape), x.dtype, valid_token_mask is not None,
+                    torch.is_inference_mode_enabled())
+        return model_key, geometry
+
+    def _drop_graphs(self) -> None:
+        self._inference_graphs.clear()
+        self._inference_graph = None
+        self._graph_model_key = None
 
     def clear_cuda_graph(self) -> None:
-        """Release the single cached capture; a later eligible call rebuilds it."""
+        """Release every cached capture; a later eligible call rebuilds what it needs."""
         with self._inference_graph_lock:
-            self._inference_graph = None
+            self._drop_graphs()
 
     def _apply(self, fn, recurse=True):
         # Device/dtype moves must not keep the old graph pool or packed weights.
