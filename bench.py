@@ -221,6 +221,8 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
     attention_bf16_d64: bf16 causal [4,2048,16,64] (the attention of the config-4 encoder)
     encoder_fp32 / encoder_bf16: config-4 encoder forward (hipGraph replay), for the
                     per-kernel split
+    linear_gelu:    fused Linear + exact GELU, bf16, the config-4 FFN input projection
+                    (tokens 8192, 1024 -> 4096)
     layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
                     among input sets that together exceed twice the 256 MB MALL
     copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
@@ -259,6 +261,14 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
             fused_residual_layer_norm(x, u, w, b, 1e-5)
 
         work = layer_norm_bytes(rows, hidden)
+    elif which == "linear_gelu":
+        from transformer_opt.kernels import linear_gelu
+
+        x = torch.randn(8192, 1024, device="cuda").to(torch.bfloat16)
+        w = (torch.randn(4096, 1024, device="cuda") * 1024 ** -0.5).to(torch.bfloat16)
+        b = (torch.randn(4096, device="cuda") * 0.1).to(torch.bfloat16)
+        fn = lambda: linear_gelu(x, w, b)  # noqa: E731
+        work = 2.0 * 8192 * 4096 * 1024
     elif which in ("encoder_fp32", "encoder_bf16"):
         from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
 
@@ -315,7 +325,8 @@ def main() -> int:
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16",
-                                                   "attention_bf16_d64", "encoder_fp32", "encoder_bf16"),
+                                                   "attention_bf16_d64", "encoder_fp32", "encoder_bf16",
+                                                   "linear_gelu"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")

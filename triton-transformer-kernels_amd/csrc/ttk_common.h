@@ -90,6 +90,17 @@ struct LnParams {
   int zero_norm;
 };
 
+// Launch parameters of the fused Linear + GELU kernel (element row strides).
+struct LinearParams {
+  const void* x;     // [M, K], row stride ldx
+  const void* w;     // [N, K], row stride ldw
+  const void* bias;  // [N] or nullptr
+  void* y;           // [M, N], row stride ldy
+  int M, N, K;
+  int ldx, ldw, ldy;
+  int tiles_m;       // set by the launcher
+};
+
 // Host-side launchers (defined next to their kernels).  Return a HIP error.
 // launch_attention fills p.pair / p.units and sizes the grid itself.
 hipError_t launch_attention(int dtype, int D, bool causal, bool has_mask,
@@ -98,5 +109,7 @@ int attention_block_m(int dtype, int D);
 
 hipError_t launch_residual_layernorm(int dtype, const LnParams& p, bool vector_path,
                                      int vectors_per_lane, hipStream_t stream);
+
+hipError_t launch_linear_gelu(int dtype, LinearParams& p, hipStream_t stream);
 
 }  // namespace ttk

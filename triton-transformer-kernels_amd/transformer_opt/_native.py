@@ -31,8 +31,9 @@ EXPORTED_SYMBOLS = (
     "ttk_last_error",
     "ttk_attention_fwd",
     "ttk_residual_layernorm_fwd",
+    "ttk_linear_gelu_fwd",
 )
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -64,6 +65,10 @@ def _configure(lib: ctypes.CDLL) -> None:
     lib.ttk_residual_layernorm_fwd.argtypes = [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int,
         _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int, _vp,
+    ]
+    lib.ttk_linear_gelu_fwd.restype = ctypes.c_int
+    lib.ttk_linear_gelu_fwd.argtypes = [
+        _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
     ]
 
 

@@ -1,6 +1,7 @@
 """gfx950 HIP kernels behind the reference's kernel-module surface."""
 
 from .attention import hip_attention, hip_available
+from .linear import linear_gelu, linear_gelu_supported
 from .residual_layer_norm import fused_residual_layer_norm, layer_norm
 
 __all__ = [
@@ -8,4 +9,6 @@ __all__ = [
     "hip_attention",
     "hip_available",
     "layer_norm",
+    "linear_gelu",
+    "linear_gelu_supported",
 ]
