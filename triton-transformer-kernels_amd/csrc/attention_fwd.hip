@@ -106,13 +106,25 @@ __device__ __forceinline__ float sum_with_other_half(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// LDS-DMA: each active lane copies 16 bytes from its own global address to
-// lds_base + 16 * lane (global_load_lds_dwordx4; lds_base is wave-uniform).
-// Completion is tracked by vmcnt only: callers wait with vm_wait() before the
-// barrier that publishes the buffer.
+// LDS-DMA: each active lane copies the 16 bytes at gbase + voff (gbase
+// wave-uniform, voff the lane's byte offset) to lds_base + 16 * lane
+// (global_load_lds_dwordx4; lds_base is wave-uniform).  Completion is tracked
+// by vmcnt only: callers wait with vm_wait() before the barrier that publishes
+// the buffer.  Issued as inline assembly: the compiler cannot tell which LDS
+// reads a copy feeds, and with the builtin it waits for every outstanding
+// copy before the first LDS read after it - here, the K read right after the
+// next tile's copies are issued.  M0 carries the LDS address; the one wait
+// state after writing it is required before the copy reads it.
 #define TTK_LDS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
-__device__ __forceinline__ void dma16(const void* gptr, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(gptr, TTK_LDS(lds_base), 16, 0, 0);
+__device__ __forceinline__ void dma16(const void* gbase, unsigned voff, void* lds_base) {
+  const unsigned lds = static_cast<unsigned>(reinterpret_cast<size_t>(TTK_LDS(lds_base)));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(gbase), "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
 }
 __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -548,31 +560,32 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
   // on the zero-padded d 8..15, which meets zero Q entries - copies chunk 0
   // again; keys past S copy row S-1 (finite data that the mask neutralises).
   // The (row, chunk) a lane copies is the same for every tile, so its element
-  // offset is computed once (row < 64 and the ABI bounds the key stride below
-  // 2^25 elements, so it fits int32); -1 marks a lane past the tile.
+  // byte offset from the tile's first key row is computed once (row < 64 and
+  // the ABI bounds the key stride below 2^25 elements, so 2 * (row * ks + col)
+  // fits 32 bits); lanes past the tile are marked by pos >= BN * KCH.
   constexpr int KCH = KS / 8;
   constexpr int NK = (BN * KCH + 63) / 64;
   constexpr int NW = kThreads / 64;
   constexpr int KPW = (NK + NW - 1) / NW;
-  int koff[KPW];
+  unsigned koff[KPW];
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     const int pos = 64 * (wave + NW * i) + lane;
     const int row = pos / KCH;
     const int cc = pos - row * KCH;
-    koff[i] = pos < BN * KCH ? row * static_cast<int>(p.ks) + 8 * (cc < CPR ? cc : 0) : -1;
+    koff[i] = 2u * static_cast<unsigned>(row * static_cast<int>(p.ks) + 8 * (cc < CPR ? cc : 0));
   }
   // V: LDS-DMA into row-major rows of VCH 16-byte chunks (read back with the
   // transposing load); pad chunks copy a data chunk of the same row again.
   constexpr int NV = (BN * VCH + 63) / 64;
   constexpr int VPW = (NV + NW - 1) / NW;
-  int voff[VPW];
+  unsigned voff[VPW];
 #pragma unroll
   for (int i = 0; i < VPW; ++i) {
     const int pos = 64 * (wave + NW * i) + lane;
     const int row = pos / VCH;
     const int cc = pos - row * VCH;
-    voff[i] = pos < BN * VCH ? row * static_cast<int>(p.vs) + 8 * (cc < CPR ? cc : cc - CPR) : -1;
+    voff[i] = 2u * static_cast<unsigned>(row * static_cast<int>(p.vs) + 8 * (cc < CPR ? cc : cc - CPR));
   }
   // Per-lane base of the transposing V reads: lane i of 16-lane group g
   // addresses key row 4*(g/2) + i/4 and d = 16*(g%2) + 4*(i%4), so lane
@@ -614,15 +627,17 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
 #pragma unroll
       for (int i = 0; i < KPW; ++i) {
         const int j = wave + NW * i;
-        if (j < NK && koff[i] >= 0) {
+        const int pos = 64 * j + lane;
+        if (j < NK && pos < BN * KCH) {
           if (!ragged) {
-            dma16(kt + koff[i], &smK[buf][512 * j]);
+            dma16(kt, koff[i], &smK[buf][512 * j]);
           } else {
-            const int pos = 64 * j + lane;
+            // Keys past S copy row S-1 (at or after the tile's first key).
             const int row = pos / KCH;
             const int cc = pos - row * KCH;
-            const int key = min(t * BN + row, S - 1);
-            dma16(K + key * p.ks + 8 * (cc < CPR ? cc : 0), &smK[buf][512 * j]);
+            const int rrel = min(t * BN + row, S - 1) - t * BN;
+            dma16(kt, 2u * static_cast<unsigned>(rrel * static_cast<int>(p.ks) + 8 * (cc < CPR ? cc : 0)),
+                  &smK[buf][512 * j]);
           }
         }
       }
@@ -642,15 +657,16 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
 #pragma unroll
       for (int i = 0; i < VPW; ++i) {
         const int j = wave + NW * i;
-        if (j < NV && voff[i] >= 0) {
+        const int pos = 64 * j + lane;
+        if (j < NV && pos < BN * VCH) {
           if (!ragged) {
-            dma16(vt + voff[i], &smV[buf][512 * j]);
+            dma16(vt, voff[i], &smV[buf][512 * j]);
           } else {
-            const int pos = 64 * j + lane;
             const int row = pos / VCH;
             const int cc = pos - row * VCH;
-            const int key = min(t * BN + row, S - 1);
-            dma16(V + key * p.vs + 8 * (cc < CPR ? cc : cc - CPR), &smV[buf][512 * j]);
+            const int rrel = min(t * BN + row, S - 1) - t * BN;
+            dma16(vt, 2u * static_cast<unsigned>(rrel * static_cast<int>(p.vs) + 8 * (cc < CPR ? cc : cc - CPR)),
+                  &smV[buf][512 * j]);
           }
         }
       }
