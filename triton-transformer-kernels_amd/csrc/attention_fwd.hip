@@ -258,6 +258,9 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
 
   // Every pass ends with a barrier after its last LDS read, so the next pass
   // may refill both buffers right away.
+  f32x4 rk[C::CPT], rv[C::CPT];
+  bool rm = false;
+  bool staged = false;  // tile 0 of the coming pass already sits in rk / rv
   for (int pass = 0; pass < w.npass; ++pass) {
     const int qb = pass == 0 ? w.q_first : w.q_second;
     const int q0 = qb * kBM + wave * 32;  // first query of this wavefront (uniform)
@@ -279,8 +282,6 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
     const int kv_end = CAUSAL ? min(S, (qb + 1) * kBM) : S;
     const int ntiles = (kv_end + BN - 1) / BN;
 
-    f32x4 rk[CPT], rv[CPT];
-    bool rm = false;
     // Global loads of tile t into registers; rows past S read as zeros.
     auto gload = [&](int t) {
       const bool full = (t + 1) * BN <= S;
@@ -433,13 +434,19 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       }
     };
 
-    gload(0);
+    if (!staged) gload(0);
     uint64_t kvalid = lstore(0, 0);
     __syncthreads();
+    staged = false;
 
     for (int t = 0; t < ntiles; ++t) {
       const int buf = t & 1;
-      if (t + 1 < ntiles) gload(t + 1);
+      if (t + 1 < ntiles) {
+        gload(t + 1);
+      } else if (pass + 1 < w.npass) {
+        gload(0);  // the next pass's key tile 0 (same head, same rows)
+        staged = true;
+      }
       const int k0 = t * BN;
       if (q0 < S && (!CAUSAL || k0 <= q0 + 31)) {
         // Leading sub-blocks that hold any key this wavefront may see.
