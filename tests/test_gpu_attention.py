@@ -156,6 +156,32 @@ def test_hip_attention_matches_explicit_reference(
         tight_check(actual, reference, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("ramp", [3.0, 7.0, 12.0])
+@pytest.mark.parametrize("causal", [True, False])
+def test_running_max_growth_across_tiles(gpu_ready, dtype, head_dim, ramp, causal):
+    # Scores rise along the key axis by about `ramp` (log2 units) per 64-key
+    # tile, so every row's running max moves in every tile.  The 16-bit
+    # kernel keeps a lagging reference max and rescales only when a row
+    # outruns it by more than 2^8: ramps of 3 and 7 rescale every few tiles
+    # (P up to 2^8 in between), 12 in every tile.  The fp32 kernel rescales
+    # every tile.  Either way the output must match the oracle.
+    g = torch.Generator().manual_seed(int(ramp * 10) + head_dim)
+    seq_len, heads = 700, 2
+    c = head_dim ** -0.5 * 1.4426950408889634
+    per_key = ramp / (64 * c)
+    keys = torch.arange(seq_len, dtype=torch.float32)
+    q = 1.0 + 0.1 * torch.randn(1, seq_len, heads, head_dim, generator=g)
+    k = (per_key / head_dim) * keys[None, :, None, None] + 0.1 * torch.randn(1, seq_len, heads, head_dim, generator=g)
+    v = torch.randn(1, seq_len, heads, head_dim, generator=g)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    actual = run_hip(q, k, v, None, causal)
+    reference = oracle(q, k, v, None, causal)
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, dtype, tol=1e-4)
+
+
 def test_all_keys_masked_is_finite_zero(gpu_ready):
     # Reference tests/test_gpu_attention.py:114-128.
     g = torch.Generator().manual_seed(3)

@@ -754,6 +754,22 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       }
     };
 
+    // Lazy reference max: probabilities are exp2((s - m_run) * c) against a
+    // per-row reference m_run that moves only when the row's max exceeds it
+    // by more than 8 / c (so P <= 2^8); the accumulator and the row sum are
+    // rescaled only then, for the whole wavefront at once.  Call after the
+    // P.V MFMAs that use the previous reference have been issued.
+    auto rebase = [&](float mt) __attribute__((always_inline)) {
+      const bool need = (mt - m_run) * c > 8.0f;  // false for two -inf
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        const float m_new = need ? mt : m_run;
+        const float alpha = fast_exp2((m_run - m_new) * c);  // 0 from -inf, else <= 1
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
+        m_run = m_new;
+      }
+    };
     auto softmax = [&](auto masked_tag, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       float mt = s[0][0];
@@ -762,10 +778,8 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
 #pragma unroll
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
       mt = max_with_other_half(mt);
-      const float m_new = fmaxf(m_run, mt);
-      const float m_use = (MASKED && m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = fast_exp2((m_run - m_use) * c);
-      const float mc = m_use * c;
+      rebase(mt);
+      const float mc = ((MASKED && m_run == -INFINITY) ? 0.0f : m_run) * c;
       float ls = 0.0f;
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
@@ -775,10 +789,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
           ls += pr;
           pn[sb * 2 + (r >> 3)][r & 7] = to_bits(T{}, pr);
         }
-      l_run = __builtin_fmaf(l_run, alpha, ls);
-#pragma unroll
-      for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
-      m_run = m_new;
+      l_run += ls;
     };
 
     // P.V of the pending tile interleaved with the softmax of s: the first
@@ -790,7 +801,8 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       constexpr int E = NSB * 16;      // score elements per lane
       constexpr int PER = E / HALF;    // elements per step in each phase
       float mt = -INFINITY;
-      float ls = 0.0f, m_new = 0.0f, m_use = 0.0f, alpha = 0.0f, mc = 0.0f;
+      float ls = 0.0f, m_use = 0.0f, alpha = 1.0f, mc = 0.0f;
+      bool rebase_any = false;
       u16x8 vr[PDV];
 #pragma unroll
       for (int i = 0; i < PDV && i < NSTEP; ++i) vr[i] = vread(buf, i);
@@ -806,10 +818,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
           }
           if (idx == HALF - 1) {
             mt = max_with_other_half(mt);
-            m_new = fmaxf(m_run, mt);
-            m_use = (MASKED && m_new == -INFINITY) ? 0.0f : m_new;
+            // The reference for this tile: rebased now only if some row needs
+            // it (the accumulator rescale waits for the last P.V step).
+            const bool need = (mt - m_run) * c > 8.0f;
+            rebase_any = __builtin_amdgcn_ballot_w64(need) != 0;
+            m_use = rebase_any && need ? mt : m_run;
             alpha = fast_exp2((m_run - m_use) * c);
-            mc = m_use * c;
+            mc = ((MASKED && m_use == -INFINITY) ? 0.0f : m_use) * c;
           }
         } else {
 #pragma unroll
@@ -822,10 +837,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         }
         fence();
       }
-      l_run = __builtin_fmaf(l_run, alpha, ls);
+      if (rebase_any) {
+        l_run *= alpha;
 #pragma unroll
-      for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
-      m_run = m_new;
+        for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
+        m_run = m_use;
+      }
+      l_run += ls;
     };
 
     dma_k(0, 0);
