@@ -151,26 +151,33 @@ def layer_norm_gbps(hidden: int, rows: int = 32768, steps: int = 50, warmup: int
     return layer_norm_bytes(rows, hidden) / (ms * 1e-3) / 1e9, ms, nsets
 
 
-def model_tokens_per_second(dtype_name: str, steps: int = 5, warmup: int = 2):
-    """Config 4: 6 layers, d=1024, H=16, FFN 4096, B=4, S=2048, causal."""
+# TransformerConfig fields: batch, seq_len, d_model, heads, ffn, layers, causal.
+ENCODER_CONFIG4 = (4, 2048, 1024, 16, 4096, 6, True)
+# Config 5b: huge batch of short sequences, fp32 (FFN 4*d, non-causal).
+ENCODER_CONFIG5B = (512, 64, 512, 8, 2048, 4, False)
+
+
+def model_tokens_per_second(dtype_name: str, cfg=ENCODER_CONFIG4, steps: int = 5, warmup: int = 2):
+    """Encoder tokens/s with hipGraph replay (config 4 by default)."""
     import torch
 
     from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
 
     dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}[dtype_name]
-    config = TransformerConfig(4, 2048, 1024, 16, 4096, 6, True)
+    config = TransformerConfig(*cfg)
+    batch, seq_len, d_model = cfg[0], cfg[1], cfg[2]
     torch.manual_seed(1234)
     model = UserOptimizedTransformer(config).to(device="cuda", dtype=dtype).eval()
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
-    x = torch.randn(4, 2048, 1024, generator=g, device="cuda").to(dtype)
+    x = torch.randn(batch, seq_len, d_model, generator=g, device="cuda").to(dtype)
     with torch.inference_mode():
         wall, ms = time_launches(lambda: model(x), steps, warmup)
         replays = model.cuda_graph_replays
     med = statistics.median(ms)
     del model
     torch.cuda.empty_cache()
-    return 4 * 2048 * 1000.0 / med, med, replays
+    return batch * seq_len * 1000.0 / med, med, replays
 
 
 def cpu_baseline(time_budget_s: float = 20.0):
@@ -432,7 +439,7 @@ def main() -> int:
                 f"non-causal {entry['noncausal']['tflops']} TF")
         secondary["attention_fp32_B8_H16_D64_sweep"] = sweep
         torch.cuda.empty_cache()
-        tf, ms = attention_tflops(1, 16384, 32, 128, True, torch.bfloat16, steps=5, warmup=2)
+        tf, ms = attention_tflops(1, 16384, 32, 128, True, torch.bfloat16, steps=10, warmup=5)
         secondary["attention_bf16_causal_B1_H32_S16384_D128"] = {
             "tflops": round(tf, 2), "ms": round(ms, 3),
             "frac_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
@@ -452,6 +459,10 @@ def main() -> int:
             model[dtype_name] = {"tokens_per_s": round(tok, 1), "ms": round(ms, 3), "graph_replays": replays}
             log(f"encoder {dtype_name}: {tok:.0f} tokens/s ({ms:.2f} ms)")
         secondary["encoder_6L_d1024_B4_S2048_causal"] = model
+        tok, ms, replays = model_tokens_per_second("fp32", ENCODER_CONFIG5B, steps=10, warmup=3)
+        secondary["encoder_5b_4L_d512_B512_S64_fp32"] = {
+            "tokens_per_s": round(tok, 1), "ms": round(ms, 3), "graph_replays": replays}
+        log(f"encoder config 5b fp32: {tok:.0f} tokens/s ({ms:.2f} ms)")
         result["secondary"] = secondary
 
     if not args.no_cpu_baseline:
