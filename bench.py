@@ -230,6 +230,7 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
                     per-kernel split
     linear_gelu:    fused Linear + exact GELU, bf16, the config-4 FFN input projection
                     (tokens 8192, 1024 -> 4096)
+    gelu:           exact GELU, bf16, the config-4 FFN activation [8192, 4096] (GB/s)
     layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
                     among input sets that together exceed twice the 256 MB MALL
     copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
@@ -276,6 +277,12 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         b = (torch.randn(4096, device="cuda") * 0.1).to(torch.bfloat16)
         fn = lambda: linear_gelu(x, w, b)  # noqa: E731
         work = 2.0 * 8192 * 4096 * 1024
+    elif which == "gelu":
+        from transformer_opt.kernels import gelu_
+
+        act = torch.randn(8192, 4096, device="cuda").to(torch.bfloat16)
+        fn = lambda: gelu_(act)  # noqa: E731
+        work = 2.0 * act.numel() * 2  # bytes: read and write once
     elif which in ("encoder_fp32", "encoder_bf16"):
         from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
 
@@ -303,7 +310,7 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         finish.record()
         torch.cuda.synchronize()
     ms = begin.elapsed_time(finish) / steps
-    if which in ("layernorm", "copy"):
+    if which in ("layernorm", "copy", "gelu"):
         rate, unit = work / (ms * 1e-3) / 1e9, "GB/s"
     elif which.startswith("encoder"):
         rate, unit = work / (ms * 1e-3), "tokens/s"
@@ -333,7 +340,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16",
                                                    "attention_bf16_d64", "encoder_fp32", "encoder_bf16",
-                                                   "linear_gelu"),
+                                                   "linear_gelu", "gelu"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")

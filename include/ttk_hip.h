@@ -1,6 +1,6 @@
 /*
  * ttk_hip.h - C ABI of the MI355X (gfx950) fused attention, fused
- * residual-add + LayerNorm and fused Linear + GELU kernels.
+ * residual-add + LayerNorm, fused Linear + GELU and exact-GELU kernels.
  *
  * Plain C: no HIP, no torch types.  Every tensor is a raw device pointer plus
  * element strides.  The caller owns all memory (inputs and outputs); the
@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TTK_ABI_VERSION 2
+#define TTK_ABI_VERSION 3
 
 typedef enum {
   TTK_OK = 0,
@@ -127,6 +127,19 @@ ttk_status ttk_linear_gelu_fwd(const void* x, const void* w, const void* bias,
                                void* y, int dtype, int64_t M, int64_t N,
                                int64_t K, int64_t ldx, int64_t ldw,
                                int64_t ldy, void* stream);
+
+/*
+ * Exact (erf) GELU, elementwise: y[i] = x[i] * Phi(x[i]) for i < n, computed
+ * in fp32 and rounded once to `dtype` (TTK_F32, TTK_BF16 or TTK_F16).  x and
+ * y are contiguous; y == x (in place) is allowed, any other overlap is
+ * TTK_EINVAL.  16-byte aligned buffers take the vector path.  n <= 2^38.
+ *
+ * Replaces the separate GELU pass of the encoder's FFN,
+ * `F.gelu(layer.ffn_in(ffn_input), approximate="none")` (reference
+ * transformer_opt/submission.py:507; benchmarks/torch_transformer_benchmark.py:
+ * 95-97), on the library GEMM's output.
+ */
+ttk_status ttk_gelu_fwd(const void* x, void* y, int dtype, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -143,3 +143,19 @@ def test_linear_gelu_argument_errors_are_reported_without_launching():
     assert f(16, 16, 12, 16, _native.TTK_BF16, 4, 8, 64, 64, 64, 8, None) == _native.TTK_EUNSUPPORTED
     assert "8-byte aligned" in _native.last_error()
     assert f(16, 16, None, 16, _native.TTK_BF16, 0, 8, 64, 64, 64, 8, None) == _native.TTK_OK
+
+
+def test_gelu_argument_errors_are_reported_without_launching():
+    lib = _native.load()
+    f = lib.ttk_gelu_fwd
+    # (x, y, dtype, n, stream)
+    assert f(16, 16, 7, 8, None) == _native.TTK_EUNSUPPORTED
+    assert "dtype" in _native.last_error()
+    assert f(16, 16, _native.TTK_BF16, -1, None) == _native.TTK_EINVAL
+    assert f(16, 16, _native.TTK_BF16, (1 << 38) + 1, None) == _native.TTK_EINVAL
+    assert f(None, 16, _native.TTK_BF16, 8, None) == _native.TTK_EINVAL
+    # y one element past x: overlapping but not in place.
+    assert f(1024, 1026, _native.TTK_BF16, 8, None) == _native.TTK_EINVAL
+    assert "overlap" in _native.last_error()
+    assert f(1024 + 16, 1024, _native.TTK_F32, 8, None) == _native.TTK_EINVAL  # 32 bytes, 16 apart
+    assert f(16, 16, _native.TTK_F32, 0, None) == _native.TTK_OK

@@ -255,3 +255,22 @@ extern "C" ttk_status ttk_linear_gelu_fwd(const void* x, const void* w, const vo
   }
   return TTK_OK;
 }
+
+extern "C" ttk_status ttk_gelu_fwd(const void* x, void* y, int dtype, int64_t n, void* stream) {
+  g_error[0] = '\0';
+  const int es = elem_bytes(dtype);
+  if (es == 0) return fail(TTK_EUNSUPPORTED, "gelu: unsupported dtype code %d", dtype);
+  if (n < 0 || n > (int64_t{1} << 38)) {
+    return fail(TTK_EINVAL, "gelu: element count %lld outside [0, 2^38]", (long long)n);
+  }
+  if (n == 0) return TTK_OK;
+  if (!x || !y) return fail(TTK_EINVAL, "gelu: x and y must not be NULL");
+  const uintptr_t xb = reinterpret_cast<uintptr_t>(x), yb = reinterpret_cast<uintptr_t>(y);
+  const uintptr_t bytes = static_cast<uintptr_t>(n) * static_cast<uintptr_t>(es);
+  if (xb != yb && xb < yb + bytes && yb < xb + bytes) {
+    return fail(TTK_EINVAL, "gelu: x and y overlap without being the same buffer");
+  }
+  const hipError_t err = ttk::launch_gelu(dtype, x, y, n, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(TTK_ELAUNCH, "gelu: launch failed: %s", hipGetErrorString(err));
+  return TTK_OK;
+}

@@ -54,6 +54,27 @@ __device__ __forceinline__ unsigned short from_f32(F16, float v) {
   return __builtin_bit_cast(unsigned short, h);
 }
 
+// gelu(v) = v * Phi(v), Phi the standard normal CDF, with
+// Phi(v) = 1 - h(|v|) (v >= 0) or h(|v|) (v < 0), h(a) = erfc(a / sqrt(2)) / 2,
+// and erfc(x) = t*(a1 + t*(a2 + t*(a3 + t*(a4 + t*a5)))) * exp(-x^2),
+// t = 1/(1 + p*x): Abramowitz & Stegun, Handbook of Mathematical Functions,
+// 7.1.26 (after Hastings), |error| <= 1.5e-7 on erf - far below the bf16 /
+// fp16 rounding of the result.  With x = |v|/sqrt(2) the factor 1/2, the
+// 1/sqrt(2) and log2(e) fold into the constants: t = 1/(1 + (p/sqrt2)|v|),
+// h = t * (a1/2 + ... ) * 2^(-v^2 log2(e) / 2).  v * (1 - h) keeps
+// gelu(+inf) = +inf and NaN in, NaN out.
+__device__ __forceinline__ float gelu_exact(float v) {
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(fabsf(v), 0.23164188826636040f, 1.0f));
+  float q = __builtin_fmaf(t, 0.5307027145f, -0.7265760135f);
+  q = __builtin_fmaf(t, q, 0.7107068705f);
+  q = __builtin_fmaf(t, q, -0.142248368f);
+  q = __builtin_fmaf(t, q, 0.127414796f);
+  const float e = __builtin_amdgcn_exp2f((v * v) * -0.72134752044448170f);
+  const float te = t * e;
+  const float phi = v >= 0.0f ? __builtin_fmaf(-te, q, 1.0f) : te * q;
+  return v * phi;
+}
+
 // Launch parameters of the attention kernels (element strides).
 struct AttnParams {
   const void* q;
@@ -111,5 +132,8 @@ hipError_t launch_residual_layernorm(int dtype, const LnParams& p, bool vector_p
                                      int vectors_per_lane, hipStream_t stream);
 
 hipError_t launch_linear_gelu(int dtype, LinearParams& p, hipStream_t stream);
+
+// Exact GELU over n contiguous elements of dtype (0 fp32, 1 bf16, 2 fp16).
+hipError_t launch_gelu(int dtype, const void* x, void* y, int64_t n, hipStream_t stream);
 
 }  // namespace ttk

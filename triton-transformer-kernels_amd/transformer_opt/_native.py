@@ -32,8 +32,9 @@ EXPORTED_SYMBOLS = (
     "ttk_attention_fwd",
     "ttk_residual_layernorm_fwd",
     "ttk_linear_gelu_fwd",
+    "ttk_gelu_fwd",
 )
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -70,6 +71,8 @@ def _configure(lib: ctypes.CDLL) -> None:
     lib.ttk_linear_gelu_fwd.argtypes = [
         _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
     ]
+    lib.ttk_gelu_fwd.restype = ctypes.c_int
+    lib.ttk_gelu_fwd.argtypes = [_vp, _vp, ctypes.c_int, _i64, _vp]
 
 
 def load() -> ctypes.CDLL:

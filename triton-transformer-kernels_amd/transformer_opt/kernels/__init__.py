@@ -1,11 +1,14 @@
 """gfx950 HIP kernels behind the reference's kernel-module surface."""
 
 from .attention import hip_attention, hip_available
+from .gelu import gelu, gelu_
 from .linear import linear_gelu, linear_gelu_supported
 from .residual_layer_norm import fused_residual_layer_norm, layer_norm
 
 __all__ = [
     "fused_residual_layer_norm",
+    "gelu",
+    "gelu_",
     "hip_attention",
     "hip_available",
     "layer_norm",

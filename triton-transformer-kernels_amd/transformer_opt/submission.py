@@ -25,7 +25,9 @@ What is MI355X-specific:
   input geometry: shape, dtype, mask presence, inference mode) are kept, so a
   caller alternating between shapes replays instead of recapturing.
 
-Projections and the FFN stay library GEMMs (hipBLASLt through F.linear).
+Projections and the FFN stay library GEMMs (hipBLASLt through F.linear); the
+FFN's exact GELU runs in place on the HIP elementwise kernel (the fused
+Linear + GELU kernel, kernels.linear_gelu, measured no faster in the model).
 The model is forward-inference only: a call with gradients enabled on
 parameters that require them raises, as there is no backward kernel.
 """
@@ -42,6 +44,7 @@ import torch.nn.functional as F
 
 from .config import ATTENTION_BACKENDS, SUPPORTED_DTYPES
 from .dispatch import attention_forward
+from .kernels.gelu import gelu_
 from .kernels.residual_layer_norm import fused_residual_layer_norm, layer_norm
 from .model import SelfAttention, TransformerBlock, TransformerConfig
 
@@ -176,7 +179,7 @@ class UserOptimizedTransformer(nn.Module):
             del normalized
             x, ffn_input = self._fused_residual_norm(x, attn_out, layer.norm2, valid_token_mask)
             del attn_out
-            ffn_out = layer.ffn_out(F.gelu(layer.ffn_in(ffn_input), approximate="none"))
+            ffn_out = layer.ffn_out(gelu_(layer.ffn_in(ffn_input)))
             del ffn_input
             is_last = index == last_index
             next_norm = self.final_norm if is_last else self.layers[index + 1].norm1
