@@ -348,8 +348,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
 
     // One tile: S^T = K.Q^T, (mask), online softmax, O^T += V^T.P^T.
     // `nlive` = number of leading 32-key sub-blocks this wavefront needs.
-    auto tile = [&](auto masked_tag, int buf, int k0, int nlive, uint64_t kvalid) {
+    // MASKED: apply the key / causal mask; PARTIAL: only the first `nlive`
+    // sub-blocks hold keys this wavefront may see (the others are skipped).
+    // Tiles with every sub-block live keep the branch-free, interleaved
+    // sub-block chains even when masked.
+    auto tile = [&](auto masked_tag, auto partial_tag, int buf, int k0, int nlive, uint64_t kvalid) {
       constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr bool PARTIAL = decltype(partial_tag)::value;
       f32x16 s[NSB];
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
@@ -357,18 +362,18 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       f32x4 kf[NSB];
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
-        if (!MASKED || sb < nlive) kf[sb] = kread(buf, sb, 0);
+        if (!PARTIAL || sb < nlive) kf[sb] = kread(buf, sb, 0);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         f32x4 kn[NSB];
         if (g + 1 < G) {
 #pragma unroll
           for (int sb = 0; sb < NSB; ++sb)
-            if (!MASKED || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
+            if (!PARTIAL || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
         }
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb) {
-          if (MASKED && sb >= nlive) continue;
+          if (PARTIAL && sb >= nlive) continue;
 #pragma unroll
           for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kf[sb][e], qf[g][e], s[sb]);
         }
@@ -405,17 +410,17 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       m_run = m_new;
       fence();
       // ---- O^T += V^T . P^T (V fragments read one k-step ahead) -----------
-      const int nsteps = (MASKED ? nlive : NSB) * 16;
+      const int nsteps = (PARTIAL ? nlive : NSB) * 16;
       VF vf = vread(buf, 0, 0);
 #pragma unroll
       for (int idx = 0; idx < NSB * 16; ++idx) {
         // Fixed trip count (fully unrolled, so s[][] stays in registers); the
         // masked path skips the k-steps of dead sub-blocks with a uniform guard.
-        if (!MASKED || idx < nsteps) {
+        if (!PARTIAL || idx < nsteps) {
           const int sb = idx >> 4;
           const int r = idx & 15;
           VF vn{};
-          if (idx + 1 < NSB * 16 && (!MASKED || idx + 1 < nsteps)) {
+          if (idx + 1 < NSB * 16 && (!PARTIAL || idx + 1 < nsteps)) {
             vn = vread(buf, (idx + 1) >> 4, (idx + 1) & 15);
           }
           const float pr = s[sb][r];
@@ -458,9 +463,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
         }
         const bool need_mask = HAS_MASK || (k0 + BN > S) || (CAUSAL && k0 + BN - 1 > q0);
         if (need_mask) {
-          tile(std::true_type{}, buf, k0, nlive, kvalid);
+          if (nlive < NSB) {
+            tile(std::true_type{}, std::true_type{}, buf, k0, nlive, kvalid);
+          } else {
+            tile(std::true_type{}, std::false_type{}, buf, k0, NSB, kvalid);
+          }
         } else {
-          tile(std::false_type{}, buf, k0, NSB, kvalid);
+          tile(std::false_type{}, std::false_type{}, buf, k0, NSB, kvalid);
         }
       }
       if (t + 1 < ntiles) kvalid = lstore(buf ^ 1, t + 1);
