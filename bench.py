@@ -460,6 +460,22 @@ def main() -> int:
             log(f"residual+LN hidden={hidden}: {gbps:.0f} GB/s")
             torch.cuda.empty_cache()
         secondary["residual_layernorm_fp32_rows32768_gbps"] = ln
+        # Narrow shapes: width-32 rows (8 rows per wavefront; 2^22 rows so a
+        # set is 268 MB) and small head dims, causal [8, 1024, 16, D].
+        gbps, ms, nsets = layer_norm_gbps(32, rows=1 << 22, steps=20)
+        secondary["residual_layernorm_fp32_hidden32_rows4194304_gbps"] = {
+            "gbps": round(gbps, 1), "us": round(ms * 1e3, 2),
+            "frac_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4), "rotating_sets": nsets}
+        log(f"residual+LN hidden=32 rows=4194304: {gbps:.0f} GB/s")
+        torch.cuda.empty_cache()
+        small = {}
+        for d_head, dt, name in ((8, torch.float16, "fp16"), (16, torch.float32, "fp32"),
+                                 (32, torch.float32, "fp32")):
+            tf, ms = attention_tflops(8, 1024, 16, d_head, True, dt)
+            small[f"D{d_head}_{name}"] = {"tflops": round(tf, 2), "ms": round(ms, 4)}
+            log(f"attention {name} causal [8,1024,16,{d_head}]: {tf:.1f} TF")
+        secondary["attention_small_head_dim_causal_B8_S1024_H16"] = small
+        torch.cuda.empty_cache()
         model = {}
         for dtype_name in ("fp32", "bf16"):
             tok, ms, replays = model_tokens_per_second(dtype_name)

@@ -207,6 +207,44 @@ def test_config4_full_size_matches_oracle_on_causal_prefix(gpu_ready, dtype):
         assert err.mean().item() <= 1e-2
 
 
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
+def test_config4_full_size_fp16_key_padding(gpu_ready, causal):
+    # fp16 with a key-padding mask at the config-4 model size (6 layers,
+    # d=1024, H=16, FFN 4096, B=4, S=2048), through the hipGraph replay path.
+    # Sequence lengths 2048, 1531, 200 and 37 put masked keys inside every
+    # checked region: causal - the oracle on the first P positions (outputs
+    # there see only keys < P); non-causal - the oracle on whole sequences of
+    # two batch elements (batch elements never interact).  Bound as for the
+    # smaller fp16 model; rows the mask invalidates are exact zeros over the
+    # whole output.
+    cfg = TransformerConfig(4, 2048, 1024, 16, 4096, 6, causal)
+    baseline, model = build(cfg, dtype=torch.float16, seed=45)
+    baseline.load_state_dict({k: v.to(torch.float16).float() for k, v in baseline.state_dict().items()})
+    lengths = torch.tensor([2048, 1531, 200, 37])
+    mask = torch.arange(2048)[None, :] < lengths[:, None]
+    x = torch.randn(4, 2048, 1024, generator=torch.Generator().manual_seed(46))
+    x = x.masked_fill(~mask[..., None], 0).to(torch.float16)
+    with torch.inference_mode():
+        out = model(x.cuda(), mask.cuda())
+        if causal:
+            prefix = 256
+            ref = baseline(x[:, :prefix].float(), mask[:, :prefix])
+            got = out[:, :prefix].float().cpu()
+        else:
+            picks = torch.tensor([1, 3])
+            ref = baseline(x[picks].float(), mask[picks])
+            got = out[picks.cuda()].float().cpu()
+    assert model.cuda_graph_replays == 1
+    assert out.dtype == torch.float16 and out.shape == (4, 2048, 1024)
+    full = out.float().cpu()
+    assert bool(torch.isfinite(full).all())
+    assert bool((full[~mask] == 0).all())
+    err = (got - ref).abs()
+    ok = (err <= 5e-2) | (err <= 0.05 * ref.abs())
+    assert bool(ok.all()), f"failed={int((~ok).sum())} max_abs={err.max().item():.3g}"
+    assert err.mean().item() <= 1e-2
+
+
 def test_config5b_huge_batch_encoder_matches_oracle_on_batch_subset(gpu_ready):
     # BASELINE config 5b at full size: B=512, S=64, d=512, H=8 (D=64), 4
     # layers, fp32, hipGraph replay.  The FFN width is not stated there; 4*d
