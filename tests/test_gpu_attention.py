@@ -209,6 +209,38 @@ def test_causal_frontier_matches_reference_at_tile_boundaries(gpu_ready, seq_len
     tight_check(actual, reference, torch.float32)
 
 
+@pytest.mark.parametrize("seq_len", [97, 127, 128, 225, 353, 384])
+@pytest.mark.parametrize("head_dim", [8, 32, 64])
+@pytest.mark.parametrize("mask_mode", ["none", "drop_last32", "only_last32"])
+def test_causal_last_diagonal_sub_block_split_between_wavefronts(gpu_ready, seq_len, head_dim, mask_mode):
+    # fp32 causal: in the last key tile of a 128-query tile, the keys
+    # [start+96, start+128) of the last 32 query rows are processed by another
+    # wavefront and merged (running max, sum and output) into those rows.
+    # Sequence lengths leave 1, 31 or 32 valid rows there; the key masks make
+    # either side of the merge empty: "drop_last32" removes those keys (the
+    # handed-over part sees no key), "only_last32" keeps only them (the rows'
+    # own part sees no key, rows before them see none at all -> zeros).
+    g = torch.Generator().manual_seed(seq_len + head_dim)
+    batch = 2
+    q = torch.randn(batch, seq_len, 2, head_dim, generator=g)
+    k, v = torch.randn(q.shape, generator=g), torch.randn(q.shape, generator=g)
+    keys = torch.arange(seq_len)
+    in_last32 = (keys % 128) >= 96
+    if mask_mode == "none":
+        mask = None
+    elif mask_mode == "drop_last32":
+        mask = (~in_last32)[None, :].expand(batch, seq_len).clone()
+    else:
+        mask = in_last32[None, :].expand(batch, seq_len).clone()
+    actual = run_hip(q, k, v, mask, True)
+    reference = oracle(q, k, v, mask, True)
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, torch.float32)
+    if mask_mode == "only_last32":
+        # Rows before the first allowed key see nothing: exact zeros.
+        assert bool((actual[:, :96] == 0).all())
+
+
 def test_causal_frontier_cannot_observe_future_key_value_tiles(gpu_ready):
     # Reference tests/test_gpu_attention.py:172-181, bitwise.
     g = torch.Generator().manual_seed(43)

@@ -240,6 +240,15 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   using VF = typename VFrag32<D>::type;
   __shared__ __attribute__((aligned(16))) float smK[2][BN * KS];
   __shared__ __attribute__((aligned(16))) float smV[2][BN * D];
+  // Causal hand-off (two-sub-block tiles): in the last key tile of a query
+  // tile only wavefronts 2 (one sub-block) and 3 (two) have keys left, so
+  // wavefront 0 - whose rows are complete by then - takes wavefront 3's
+  // diagonal sub-block and passes its partial state through smX: per lane
+  // 16*DB accumulator values, the row max and the lane half's row sum, as
+  // 16-byte chunks at smX[(chunk * 64 + lane) * 4].
+  constexpr bool kHandoff = CAUSAL && NSB == 2;
+  constexpr int NX4 = 4 * DB + 1;
+  __shared__ __attribute__((aligned(16))) float smX[kHandoff ? NX4 * 256 : 4];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -264,7 +273,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   for (int pass = 0; pass < w.npass; ++pass) {
     const int qb = pass == 0 ? w.q_first : w.q_second;
     const int q0 = qb * kBM + wave * 32;  // first query of this wavefront (uniform)
-    const int qrow = q0 + m;              // query of this lane
+    int qrow = q0 + m;                    // query of this lane (wavefront 3's on a hand-off)
 
     // B operand of S^T = K.Q^T: group g covers d = 8g..8g+7, lane half h
     // holds d = 8g+4h..8g+4h+3 (one element per k-step).  Pre-scaled into
@@ -281,6 +290,10 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
 
     const int kv_end = CAUSAL ? min(S, (qb + 1) * kBM) : S;
     const int ntiles = (kv_end + BN - 1) / BN;
+    // Hand-off in this pass: the last tile starts half-way into the query
+    // tile and wavefront 3 has rows (and keys of its second sub-block) < S.
+    const bool handoff = kHandoff && (ntiles - 1) * BN == qb * kBM + 64 && qb * kBM + 96 < S;
+    bool own_done = false;  // wavefront 0 stored its own rows early
 
     // Global loads of tile t into registers; rows past S read as zeros.
     auto gload = [&](int t) {
@@ -352,9 +365,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
     // sub-blocks hold keys this wavefront may see (the others are skipped).
     // Tiles with every sub-block live keep the branch-free, interleaved
     // sub-block chains even when masked.
-    auto tile = [&](auto masked_tag, auto partial_tag, int buf, int k0, int nlive, uint64_t kvalid) {
+    // SB0: index in the LDS tile of the first sub-block processed (k0 and
+    // kvalid describe that sub-block onwards).
+    auto tile = [&](auto masked_tag, auto partial_tag, auto sb0_tag, int buf, int k0, int nlive,
+                    uint64_t kvalid) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       constexpr bool PARTIAL = decltype(partial_tag)::value;
+      constexpr int SB0 = decltype(sb0_tag)::value;
       f32x16 s[NSB];
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
@@ -362,14 +379,14 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       f32x4 kf[NSB];
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
-        if (!PARTIAL || sb < nlive) kf[sb] = kread(buf, sb, 0);
+        if (!PARTIAL || sb < nlive) kf[sb] = kread(buf, SB0 + sb, 0);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         f32x4 kn[NSB];
         if (g + 1 < G) {
 #pragma unroll
           for (int sb = 0; sb < NSB; ++sb)
-            if (!PARTIAL || sb < nlive) kn[sb] = kread(buf, sb, g + 1);
+            if (!PARTIAL || sb < nlive) kn[sb] = kread(buf, SB0 + sb, g + 1);
         }
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb) {
@@ -411,7 +428,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       fence();
       // ---- O^T += V^T . P^T (V fragments read one k-step ahead) -----------
       const int nsteps = (PARTIAL ? nlive : NSB) * 16;
-      VF vf = vread(buf, 0, 0);
+      VF vf = vread(buf, SB0, 0);
 #pragma unroll
       for (int idx = 0; idx < NSB * 16; ++idx) {
         // Fixed trip count (fully unrolled, so s[][] stays in registers); the
@@ -421,7 +438,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
           const int r = idx & 15;
           VF vn{};
           if (idx + 1 < NSB * 16 && (!PARTIAL || idx + 1 < nsteps)) {
-            vn = vread(buf, (idx + 1) >> 4, (idx + 1) & 15);
+            vn = vread(buf, SB0 + ((idx + 1) >> 4), (idx + 1) & 15);
           }
           const float pr = s[sb][r];
           if constexpr (DB == 1) {
@@ -439,6 +456,32 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       }
     };
 
+    // O = acc / l for this lane's row.
+    auto epilogue = [&]() __attribute__((always_inline)) {
+      const float lt = sum_with_other_half(l_run);
+      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+      if (qrow < S) {
+        float* __restrict__ O = static_cast<float*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+          // Block i of the accumulator holds d = DB*row + i; register 4*j4+e
+          // holds row 8*j4 + 4h + e, so a lane's d-values form one run of 4*DB.
+          const int d0 = DB * (8 * j4 + 4 * h);
+          if (D < 32 && d0 >= D) continue;
+          float vals[4 * DB];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int i = 0; i < DB; ++i) vals[DB * e + i] = acc[i][4 * j4 + e] * inv;
+#pragma unroll
+          for (int c = 0; c < DB; ++c) {
+            *reinterpret_cast<f32x4*>(O + d0 + 4 * c) =
+                f32x4{vals[4 * c], vals[4 * c + 1], vals[4 * c + 2], vals[4 * c + 3]};
+          }
+        }
+      }
+    };
+
     if (!staged) gload(0);
     uint64_t kvalid = lstore(0, 0);
     __syncthreads();
@@ -453,7 +496,39 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
         staged = true;
       }
       const int k0 = t * BN;
-      if (q0 < S && (!CAUSAL || k0 <= q0 + 31)) {
+      if constexpr (kHandoff) {
+        if (handoff && t == ntiles - 1 && wave == 0) {
+          // Own rows are complete (their last keys were in tile t - 1): store
+          // them, then run wavefront 3's second sub-block of this tile on
+          // wavefront 3's rows from a fresh state and hand the state over.
+          const int frow = qb * kBM + 96 + m;
+          f32x4 fq[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            fq[g] = frow < S ? *reinterpret_cast<const f32x4*>(Q + frow * p.qs + 8 * g + 4 * h) * p.scale_log2
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+          epilogue();
+          own_done = true;
+          qrow = frow;
+#pragma unroll
+          for (int g = 0; g < G; ++g) qf[g] = fq[g];
+          m_run = -INFINITY;
+          l_run = 0.0f;
+#pragma unroll
+          for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
+          tile(std::true_type{}, std::true_type{}, std::integral_constant<int, 1>{}, buf, k0 + 32, 1,
+               kvalid >> 32);
+#pragma unroll
+          for (int j = 0; j < 4 * DB; ++j) {
+            const int i = j >> 2, r0 = 4 * (j & 3);
+            *reinterpret_cast<f32x4*>(&smX[(j * 64 + lane) * 4]) =
+                f32x4{acc[i][r0], acc[i][r0 + 1], acc[i][r0 + 2], acc[i][r0 + 3]};
+          }
+          *reinterpret_cast<f32x4*>(&smX[(4 * DB * 64 + lane) * 4]) = f32x4{m_run, l_run, 0.f, 0.f};
+        }
+      }
+      if (q0 < S && (!CAUSAL || k0 <= q0 + 31) && !own_done) {
         // Leading sub-blocks that hold any key this wavefront may see.
         int nlive = NSB;
 #pragma unroll
@@ -461,44 +536,50 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
           const int ks = k0 + sb * 32;
           if (ks >= S || (CAUSAL && ks > q0 + 31)) nlive = sb;
         }
+        // On a hand-off wavefront 3 keeps only the first sub-block of the last
+        // tile; its second sub-block's keys are cleared from the valid bits,
+        // since the causal mask alone would leave them at score 0.
+        uint64_t kv = kvalid;
+        if (kHandoff && handoff && t == ntiles - 1 && wave == 3) {
+          nlive = 1;
+          kv &= 0xffffffffull;
+        }
         const bool need_mask = HAS_MASK || (k0 + BN > S) || (CAUSAL && k0 + BN - 1 > q0);
         if (need_mask) {
           if (nlive < NSB) {
-            tile(std::true_type{}, std::true_type{}, buf, k0, nlive, kvalid);
+            tile(std::true_type{}, std::true_type{}, std::integral_constant<int, 0>{}, buf, k0, nlive, kv);
           } else {
-            tile(std::true_type{}, std::false_type{}, buf, k0, NSB, kvalid);
+            tile(std::true_type{}, std::false_type{}, std::integral_constant<int, 0>{}, buf, k0, NSB, kv);
           }
         } else {
-          tile(std::false_type{}, std::false_type{}, buf, k0, NSB, kvalid);
+          tile(std::false_type{}, std::false_type{}, std::integral_constant<int, 0>{}, buf, k0, NSB, kvalid);
         }
       }
       if (t + 1 < ntiles) kvalid = lstore(buf ^ 1, t + 1);
       __syncthreads();
     }
 
-    // ---- epilogue: O = acc / l ----------------------------------------------
-    const float lt = sum_with_other_half(l_run);
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    if (qrow < S) {
-      float* __restrict__ O = static_cast<float*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
+    if constexpr (kHandoff) {
+      if (handoff && wave == 3) {
+        // Merge wavefront 0's state for the second sub-block of the last
+        // tile (written before the loop's final barrier).
+        const f32x4 ml = *reinterpret_cast<const f32x4*>(&smX[(4 * DB * 64 + lane) * 4]);
+        const float mx = fmaxf(m_run, ml[0]);
+        const float mu = mx == -INFINITY ? 0.0f : mx;
+        const float a = fast_exp2(m_run - mu);
+        const float bb = fast_exp2(ml[0] - mu);
+        l_run = __builtin_fmaf(l_run, a, ml[1] * bb);
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        // Block i of the accumulator holds d = DB*row + i; register 4*j4+e
-        // holds row 8*j4 + 4h + e, so a lane's d-values form one run of 4*DB.
-        const int d0 = DB * (8 * j4 + 4 * h);
-        if (D < 32 && d0 >= D) continue;
-        float vals[4 * DB];
+        for (int j = 0; j < 4 * DB; ++j) {
+          const int i = j >> 2, r0 = 4 * (j & 3);
+          const f32x4 x = *reinterpret_cast<const f32x4*>(&smX[(j * 64 + lane) * 4]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int i = 0; i < DB; ++i) vals[DB * e + i] = acc[i][4 * j4 + e] * inv;
-#pragma unroll
-        for (int c = 0; c < DB; ++c) {
-          *reinterpret_cast<f32x4*>(O + d0 + 4 * c) =
-              f32x4{vals[4 * c], vals[4 * c + 1], vals[4 * c + 2], vals[4 * c + 3]};
+          for (int e = 0; e < 4; ++e) acc[i][r0 + e] = __builtin_fmaf(acc[i][r0 + e], a, x[e] * bb);
         }
+        m_run = mx;
       }
     }
+    if (!own_done) epilogue();
   }
 }
 
