@@ -1006,21 +1006,40 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     for (int t = max(1, n_full); t < ntiles; ++t) generic_tile(t);
     if (pending) pv((ntiles - 1) & 1, pend_live);
 
+    // Output through LDS: the accumulator layout gives a lane 4 consecutive
+    // d of one query per register group, so direct stores would write 16
+    // bytes into each of 32 rows per instruction (partial cache lines).  The
+    // wavefront's 32 x D tile goes to its own slice of the K buffers instead
+    // (no K read or copy is pending after the loop's last barrier) and comes
+    // back as whole 16-byte row chunks, so each store covers whole rows.
     const float lt = sum_with_other_half(l_run);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    if (qrow < S) {
-      St* __restrict__ O = static_cast<St*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
+    constexpr int OS = D + 8;  // staged row stride (elements; 16-byte pad)
+    static_assert(4 * 32 * OS <= 2 * BN * KS, "output staging fits the K buffers");
+    unsigned short* so = &smK[0][0] + wave * 32 * OS;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int j4 = 0; j4 < 4; ++j4) {
-          const int d0 = 32 * db + 8 * j4 + 4 * h;  // 4 consecutive d-rows
-          if (D < 32 && d0 >= D) continue;
-          u16x4 o;
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const int d0 = 32 * db + 8 * j4 + 4 * h;  // 4 consecutive d-rows
+        if (D < 32 && d0 >= D) continue;
+        u16x4 o;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = to_bits(T{}, acc[db][4 * j4 + e] * inv);
-          *reinterpret_cast<u16x4*>(O + d0) = o;
-        }
+        for (int e = 0; e < 4; ++e) o[e] = to_bits(T{}, acc[db][4 * j4 + e] * inv);
+        *reinterpret_cast<u16x4*>(so + m * OS + d0) = o;
+      }
+    __builtin_amdgcn_wave_barrier();
+    constexpr int OCH = D / 8;  // 16-byte chunks per output row
+    St* __restrict__ O = static_cast<St*>(p.out) + b * p.ob + hh * p.oh;
+#pragma unroll
+    for (int i0 = 0; i0 < 32 * OCH; i0 += 64) {
+      const int i = i0 + lane;
+      const int row = i / OCH;
+      const int cc = i - row * OCH;
+      if ((32 * OCH % 64 == 0 || i < 32 * OCH) && q0 + row < S) {
+        *reinterpret_cast<u16x8*>(O + (q0 + row) * p.os + 8 * cc) =
+            *reinterpret_cast<const u16x8*>(so + row * OS + 8 * cc);
+      }
     }
   }
 }
