@@ -228,6 +228,8 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
     attention_bf16_d64: bf16 causal [4,2048,16,64] (the attention of the config-4 encoder)
     encoder_fp32 / encoder_bf16: config-4 encoder forward (hipGraph replay), for the
                     per-kernel split
+    encoder_5b:     config-5b encoder forward (fp32, B=512, S=64, d=512, 4 layers,
+                    hipGraph replay), for the per-kernel split
     linear_gelu:    fused Linear + exact GELU, bf16, the config-4 FFN input projection
                     (tokens 8192, 1024 -> 4096)
     gelu:           exact GELU, bf16, the config-4 FFN activation [8192, 4096] (GB/s)
@@ -293,6 +295,14 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         x = torch.randn(4, 2048, 1024, device="cuda").to(dtype)
         fn = lambda: model(x)  # noqa: E731
         work = 4 * 2048  # tokens
+    elif which == "encoder_5b":
+        from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
+
+        torch.manual_seed(1234)
+        model = UserOptimizedTransformer(TransformerConfig(*ENCODER_CONFIG5B)).to(device="cuda").eval()
+        x = torch.randn(ENCODER_CONFIG5B[0], ENCODER_CONFIG5B[1], ENCODER_CONFIG5B[2], device="cuda")
+        fn = lambda: model(x)  # noqa: E731
+        work = ENCODER_CONFIG5B[0] * ENCODER_CONFIG5B[1]  # tokens
     else:
         src = torch.empty(64 * 1024 * 1024, device="cuda")
         dst = torch.empty_like(src)
@@ -340,7 +350,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16",
                                                    "attention_bf16_d64", "encoder_fp32", "encoder_bf16",
-                                                   "linear_gelu", "gelu"),
+                                                   "encoder_5b", "linear_gelu", "gelu"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")
