@@ -92,7 +92,7 @@ CONTRACT = {
 }
 
 
-def contract_failures(actual: torch.Tensor, reference: torch.Tensor) -> int:
+def contract_failures(actual: torch.Tensor, reference: torch.Tensor, bf16_mean: float = 1e-3) -> int:
     """Elements outside the dtype's contract (finite and |d|<=atol or <=rtol*|ref|)."""
     atol, rtol = CONTRACT[actual.dtype]
     a = actual.float().cpu()
@@ -100,7 +100,7 @@ def contract_failures(actual: torch.Tensor, reference: torch.Tensor) -> int:
     err = (a - r).abs()
     ok = torch.isfinite(a) & ((err <= atol) | (err <= rtol * r.abs()))
     if actual.dtype == torch.bfloat16 and err.numel():
-        assert err.mean().item() <= 1e-3, f"bf16 mean abs error {err.mean().item():.3g}"
+        assert err.mean().item() <= bf16_mean, f"bf16 mean abs error {err.mean().item():.3g}"
     return int((~ok).sum().item())
 
 
@@ -328,6 +328,44 @@ def test_explicit_scale_and_non_power_of_two_batch_heads(gpu_ready):
         # Logits up to ~14x the default scale: fp32 rounding of the scores
         # grows with |logit|, so the tight bound scales with it.
         tight_check(actual, reference, torch.float32, tol=2e-5 * scale / 0.125)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("mask_mode", ["none", "prefix"])
+def test_negative_zero_and_large_scales(gpu_ready, dtype, head_dim, causal, mask_mode):
+    # A negative scale is folded into Q (an exact sign flip for 16-bit inputs,
+    # the pre-scale for fp32); scale 0 gives uniform weights, so every output
+    # row is the mean of V over its allowed keys (a closed form, checked
+    # without the oracle; rows with no allowed key are zero); 0.9 makes
+    # logits ~7x the default scale's.
+    g = torch.Generator().manual_seed(31 + head_dim)
+    shape = (2, 150, 3, head_dim)
+    q, k, v = (torch.randn(shape, generator=g).to(dtype) for _ in range(3))
+    mask = make_mask(mask_mode, shape[0], shape[1])
+    for scale in (-0.4, 0.0, 0.9):
+        actual = run_hip(q, k, v, mask, causal, scale=scale)
+        reference = oracle(q, k, v, mask, causal, scale=scale)
+        # bf16 rounds P and the output to 8 significant bits, so the mean
+        # error grows with |out|: at scale 0.9 the softmax is peaked and the
+        # outputs are about |v|, not an average over many keys.
+        bf16_mean = 1e-3 + 2e-3 * reference.abs().mean().item()
+        assert contract_failures(actual, reference, bf16_mean) == 0, f"scale={scale}"
+        if scale == 0.0:
+            keys = torch.ones(shape[0], shape[1], dtype=torch.bool) if mask is None else mask
+            allowed = keys[:, None, :].expand(shape[0], shape[1], shape[1])  # [b, query, key]
+            if causal:
+                allowed = allowed & torch.ones(shape[1], shape[1], dtype=torch.bool).tril()[None]
+            w = allowed.double()
+            counts = w.sum(dim=2, keepdim=True)
+            vf = v.double().reshape(shape[0], shape[1], -1)
+            mean = torch.matmul(w / counts.clamp(min=1), vf).reshape(shape)
+            err = (actual.double() - mean).abs().max().item()
+            # P is exactly 1 for every allowed key; the only rounding is the
+            # P.V accumulation in fp32 and the output conversion.
+            bound = 1e-5 if dtype == torch.float32 else (8e-3 if dtype == torch.bfloat16 else 1e-3)
+            assert err <= bound, f"scale=0 mean-of-V error {err:.3g}"
 
 
 @pytest.mark.parametrize("seq_len", [1024, 4096])

@@ -648,7 +648,11 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
   // The row max is taken on raw scores, which needs a positive scale: a
   // negative scale is folded into Q as an exact sign flip.
   const bool negate = p.scale_log2 < 0.0f;
-  const float c = negate ? -p.scale_log2 : p.scale_log2;
+  float c = negate ? -p.scale_log2 : p.scale_log2;
+  // Scale 0 (uniform weights): masked scores are -inf and -inf * 0 is NaN,
+  // so 2^-100 stands in.  Masked scores stay -inf, and every allowed score
+  // (|s| < 2^75) gives an exp2 argument below 2^-25, so P = 1 exactly.
+  if (c == 0.0f) c = 0x1p-100f;
   const unsigned short sign = negate ? 0x8000u : 0u;
 
   // K: LDS-DMA into padded rows of KCH 16-byte chunks; DMA instruction j
