@@ -368,6 +368,39 @@ def test_negative_zero_and_large_scales(gpu_ready, dtype, head_dim, causal, mask
             assert err <= bound, f"scale=0 mean-of-V error {err:.3g}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+def test_permuted_layouts_and_strided_mask(gpu_ready, dtype, causal):
+    # Q is the transpose of a [B, H, S, D] tensor, K a permute of [S, B, H, D]
+    # (every B/S/H stride differs from the packed layout), V contiguous, and
+    # the key mask a stride-2 view - all built on the GPU so no copy makes
+    # them contiguous.  The result must be bitwise the one of contiguous
+    # copies and within the contract of the oracle.
+    g = torch.Generator().manual_seed(57)
+    B, S, H, D = 2, 200, 3, 64
+    dev = torch.device("cuda")
+    q = torch.randn(B, H, S, D, generator=g).to(dtype).to(dev).transpose(1, 2)
+    k = torch.randn(S, B, H, D, generator=g).to(dtype).to(dev).permute(1, 0, 2, 3)
+    v = torch.randn(B, S, H, D, generator=g).to(dtype).to(dev)
+    mask_full = torch.rand(B, 2 * S, generator=g) > 0.25
+    mask_full[:, 0] = True
+    mask = mask_full.to(dev)[:, ::2]
+    assert not q.is_contiguous() and not k.is_contiguous() and not mask.is_contiguous()
+    actual = run_hip(q, k, v, mask, causal)
+    again = run_hip(q.contiguous(), k.contiguous(), v, mask.contiguous(), causal)
+    assert torch.equal(actual, again)
+    reference = oracle(q.cpu(), k.cpu(), v.cpu(), mask.cpu(), causal)
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, dtype)
+
+
+def test_empty_batch_returns_empty(gpu_ready):
+    for dtype in (torch.float32, torch.bfloat16):
+        q = torch.empty(0, 16, 2, 64, dtype=dtype)
+        out = run_hip(q, q, q, None, True)
+        assert out.shape == (0, 16, 2, 64) and out.dtype == dtype
+
+
 @pytest.mark.parametrize("seq_len", [1024, 4096])
 def test_baseline_size_rows_match_chunked_oracle(gpu_ready, seq_len):
     # BASELINE config 2 geometry (B=8, H=16, D=64, fp32); the oracle checks a

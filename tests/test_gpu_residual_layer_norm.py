@@ -139,3 +139,38 @@ def test_layer_norm_only_entry(gpu_ready):
         y = layer_norm(x.cuda(), w.cuda(), b.cuda(), 1e-5).cpu()
     torch.testing.assert_close(y, torch.nn.functional.layer_norm(x, (512,), w, b, 1e-5),
                                rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("hidden", [1, 3, 5, 33, 77, 255])
+def test_odd_widths_take_the_unaligned_path(gpu_ready, dtype, hidden):
+    # Rows that are not whole 16-byte vectors use the block-per-row kernel.
+    # Width 1 has zero variance, so the normalized output is beta exactly.
+    g = torch.Generator().manual_seed(hidden + 7)
+    rows = 41
+    x = torch.randn(rows, hidden, generator=g).to(dtype)
+    u = torch.randn(x.shape, generator=g).to(dtype)
+    w = (torch.rand(hidden, generator=g) + 0.5).to(dtype)
+    b = (torch.randn(hidden, generator=g) * 0.1).to(dtype)
+    mask = torch.rand(rows, generator=g) > 0.3
+    er, ey = explicit_residual_layer_norm(x, u, w, b, 1e-5, mask,
+                                          zero_invalid_residual=True, zero_invalid_normalized=True)
+    r, y = run_hip(x, u, w, b, 1e-5, mask, True, True)
+    torch.testing.assert_close(r, er, rtol=0, atol=0)
+    tol = {torch.float32: 1e-5, torch.bfloat16: 1.6e-2, torch.float16: 2e-3}[dtype]
+    torch.testing.assert_close(y.float(), ey.float(), rtol=tol, atol=tol)
+    if hidden == 1:
+        assert torch.equal(y[mask], b.expand(rows, 1)[mask])
+        assert bool((y[~mask] == 0).all())
+
+
+def test_zero_rows_return_empty_outputs(gpu_ready):
+    from transformer_opt.kernels import layer_norm
+
+    for dtype in (torch.float32, torch.bfloat16):
+        x = torch.empty(0, 64, dtype=dtype)
+        w = torch.ones(64, dtype=dtype)
+        r, y = run_hip(x, x, w, None, 1e-5, None)
+        assert r.shape == (0, 64) and y.shape == (0, 64)
+        with torch.inference_mode():
+            assert layer_norm(x.cuda(), w.cuda(), None, 1e-5).shape == (0, 64)
