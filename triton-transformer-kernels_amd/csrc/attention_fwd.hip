@@ -270,6 +270,15 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   f32x4 rk[C::CPT], rv[C::CPT];
   bool rm = false;
   bool staged = false;  // tile 0 of the coming pass already sits in rk / rv
+  // Wave priority alternates tile by tile, in opposite phase for workgroups
+  // whose index differs by the CU count.  The first grid fills every CU with
+  // workgroups i and i + CUs; left to the age order, the older of the two
+  // wins every issue conflict and finishes ~15 % earlier, and the younger
+  // one runs alone to the end.  Alternating shares the CU evenly; a lone
+  // workgroup keeps its CU nearly as busy, so the gain is small (~1 % at
+  // S=1024).
+  const int prio_phase = (static_cast<int>(blockIdx.x) / max(p.cu_count, 1)) & 1;
+  int tiles_done = 0;
   for (int pass = 0; pass < w.npass; ++pass) {
     const int qb = pass == 0 ? w.q_first : w.q_second;
     const int q0 = qb * kBM + wave * 32;  // first query of this wavefront (uniform)
@@ -489,6 +498,11 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
 
     for (int t = 0; t < ntiles; ++t) {
       const int buf = t & 1;
+      if (((tiles_done + t) & 1) == prio_phase) {
+        __builtin_amdgcn_s_setprio(1);
+      } else {
+        __builtin_amdgcn_s_setprio(0);
+      }
       if (t + 1 < ntiles) {
         gload(t + 1);
       } else if (pass + 1 < w.npass) {
@@ -580,7 +594,9 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       }
     }
     if (!own_done) epilogue();
+    tiles_done += ntiles;
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // ----------------------------------------------------------------------------
@@ -1073,6 +1089,7 @@ hipError_t launch_d(int dtype, AttnParams& p, hipStream_t stream) {
   p.pair = (dtype == 0 && CAUSAL && p.nq >= 2 &&
             paired >= static_cast<int64_t>(device_cu_count()) * kMinWaves<true, D>) ? 1 : 0;
   p.units = p.pair ? (p.nq + 1) / 2 : p.nq;
+  p.cu_count = device_cu_count();
   const dim3 g(static_cast<unsigned>(p.units) * static_cast<unsigned>(p.BH)), blk(kThreads);
   switch (dtype) {
     case 0: attn_fwd_f32_kernel<D, CAUSAL, HAS_MASK><<<g, blk, 0, stream>>>(p); break;

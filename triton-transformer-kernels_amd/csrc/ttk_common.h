@@ -92,6 +92,7 @@ struct AttnParams {
   int xcd_swizzle;   // 1 when BH % 8 == 0: heads are pinned to XCDs
   int pair;          // causal: a workgroup runs query tiles nq-1-i and i
   int units;         // workgroups per (batch, head)
+  int cu_count;      // compute units of the device (wave-priority phase)
 };
 
 // Launch parameters of the residual + LayerNorm kernels.
