@@ -28,8 +28,9 @@
 //       The fp32 MFMA is 16 passes long, so the matrix core is the bound and
 //       the softmax VALU of one wavefront runs under the MFMAs of the other
 //       wavefront on the SIMD.
-//     - bf16/fp16: the 8-pass MFMA leaves the softmax VALU (and v_exp_f32,
-//       which does not issue alongside MFMA) as the bound, so the loop is
+//     - bf16/fp16: the 8-pass MFMA leaves the softmax as the bound (per tile
+//       a wavefront issues 32 MFMAs against ~110 VALU instructions and 32
+//       v_exp_f32), so the loop is
 //       software-pipelined: iteration t computes S(t) = K(t).Q^T and then one
 //       instruction stream interleaving the P.V MFMAs of tile t-1 with the
 //       softmax of tile t.  K(t+1) and V(t) are copied global->LDS by LDS-DMA
@@ -41,6 +42,10 @@
 //   mask) take the masked path; interior tiles run unmasked.  Causal
 //   workgroups stop at their diagonal (future tiles are never loaded) and a
 //   wavefront skips the 32-key sub-blocks entirely after its last query.
+//   fp32 with 64-key tiles: in the last tile of a query tile, wavefront 0
+//   (whose rows are complete) takes wavefront 3's diagonal sub-block and
+//   hands its partial softmax state over through LDS, so the diagonal costs
+//   3 sub-block times instead of 4.
 // * Scheduling: causal query tile i costs i+1 key blocks.  When the grid
 //   still fills every workgroup slot of the GPU, a workgroup runs the query
 //   tiles nq-1-i and i one after the other, so all workgroups carry the same
@@ -48,7 +53,11 @@
 //   is ordered heaviest query tile first.  When B*H is a multiple of 8 all
 //   workgroups of one head run on the same XCD (workgroups are dealt
 //   round-robin to the 8 XCDs), so a head's K/V is fetched from HBM into one
-//   XCD's L2 instead of eight.
+//   XCD's L2 instead of eight.  The fp32 kernel alternates wave priority per
+//   tile between the two workgroups of a CU (the age order otherwise favours
+//   the older one throughout).
+// * Output: the 16-bit kernel stages each wavefront's 32 x D tile in LDS so
+//   that each store covers whole rows; fp32 stores straight from registers.
 //
 // fp32 path: v_mfma_f32_32x32x2_f32 (IEEE fp32 products, fp32 accumulate).
 // Q is pre-multiplied by scale*log2(e) so scores are already in the exp2
