@@ -174,3 +174,20 @@ def test_zero_rows_return_empty_outputs(gpu_ready):
         assert r.shape == (0, 64) and y.shape == (0, 64)
         with torch.inference_mode():
             assert layer_norm(x.cuda(), w.cuda(), None, 1e-5).shape == (0, 64)
+
+
+@pytest.mark.parametrize("rows", [1, 7, 8, 9, 4099])
+@pytest.mark.parametrize("bias", [True, False])
+def test_short_layer_norm_width_32(gpu_ready, rows, bias):
+    # The reference's width-32 entry point (residual_layer_norm.py:129-156):
+    # within float32 rounding of F.layer_norm, including row counts that are
+    # not a multiple of the eight rows a wavefront takes.
+    from transformer_opt.kernels import short_layer_norm
+
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, 32, generator=g) * 3.0
+    w = torch.randn(32, generator=g)
+    b = torch.randn(32, generator=g) if bias else None
+    with torch.inference_mode():
+        y = short_layer_norm(x.cuda(), w.cuda(), None if b is None else b.cuda(), 3e-4).cpu()
+    torch.testing.assert_close(y, torch.nn.functional.layer_norm(x, (32,), w, b, 3e-4), rtol=1e-5, atol=1e-5)

@@ -134,6 +134,20 @@ def test_fp16_model_within_stated_bound(gpu_ready, padding):
         assert bool((out.float().cpu()[~mask] == 0).all())
 
 
+def test_run_accuracy_tests_harness(gpu_ready, capsys):
+    # The reference's accuracy loop (submission.py:726-800) as its tests call
+    # it: the oracle baseline and the HIP model on the GPU, seeded cases with
+    # key padding, the organizer's OR rule on every element.
+    from transformer_opt.submission import run_accuracy_tests
+
+    cfg = TransformerConfig(2, 96, 128, 8, 512, 2, True)
+    baseline, model = build(cfg, seed=12)
+    baseline = baseline.cuda()
+    assert run_accuracy_tests(baseline, model, cfg, torch.device("cuda"), torch.float32, trials=3, seed=70,
+                              padding_ratio=0.3, input_scale=1.0, rtol=0.01, atol=1e-3)
+    assert "summary: PASS" in capsys.readouterr().out
+
+
 def test_explicit_all_valid_mask_matches_no_mask(gpu_ready):
     cfg = TransformerConfig(2, 33, 64, 4, 128, 1, True)
     _, model = build(cfg, execution_mode="eager")

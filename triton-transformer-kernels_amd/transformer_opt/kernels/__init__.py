@@ -1,9 +1,9 @@
 """gfx950 HIP kernels behind the reference's kernel-module surface."""
 
-from .attention import hip_attention, hip_available
+from .attention import hip_attention, hip_available, triton_attention, triton_available
 from .gelu import gelu, gelu_
 from .linear import linear_gelu, linear_gelu_supported
-from .residual_layer_norm import fused_residual_layer_norm, layer_norm
+from .residual_layer_norm import fused_residual_layer_norm, layer_norm, short_layer_norm
 
 __all__ = [
     "fused_residual_layer_norm",
@@ -14,4 +14,7 @@ __all__ = [
     "layer_norm",
     "linear_gelu",
     "linear_gelu_supported",
+    "short_layer_norm",
+    "triton_attention",
+    "triton_available",
 ]

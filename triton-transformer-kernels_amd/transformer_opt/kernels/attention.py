@@ -94,3 +94,10 @@ def hip_attention(
         )
     _native.check(status, "HIP attention")
     return out
+
+
+# The reference's names for the same entry points (its kernels package exports
+# triton_attention and triton_available, transformer_opt/kernels/__init__.py),
+# so callers written against it run unchanged; there is no Triton here.
+triton_attention = hip_attention
+triton_available = hip_available

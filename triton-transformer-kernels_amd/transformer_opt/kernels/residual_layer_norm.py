@@ -6,7 +6,9 @@
 ``RuntimeError`` when the kernel library is missing.  The HIP kernel also
 accepts bf16 and fp16 rows (fp32 statistics), which the reference kernel did
 not.  ``layer_norm`` is the same kernel without an update or residual output,
-used for the first norm of the fused model route.
+used for the first norm of the fused model route; ``short_layer_norm`` keeps
+the reference's entry point for rows of exactly 32 values (eight rows per
+wavefront here too) on the same kernel.
 """
 
 from __future__ import annotations
@@ -137,3 +139,36 @@ def layer_norm(
         return out
     _launch(x, None, weight, bias, eps, None, None, out, False, False)
     return out
+
+
+def short_layer_norm(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor],
+    eps: float,
+) -> torch.Tensor:
+    """Inference LayerNorm of contiguous float32 rows of exactly 32 values.
+
+    The reference entry point of the same name
+    (transformer_opt/kernels/residual_layer_norm.py:129-156) and its
+    contract: ``ValueError`` unless ``x`` is a contiguous device float32
+    tensor of rank >= 2 with last dimension 32, gradients are disabled and
+    ``weight`` (required) and ``bias`` are contiguous ``[32]`` tensors of the
+    same device and dtype.  It runs the general HIP LayerNorm kernel, whose
+    narrow-row form already gives eight such rows to one wavefront; results
+    are within float32 rounding of ``F.layer_norm``, not bit-identical to a
+    particular vendor reduction order.
+    """
+    _native.load()
+    if (x.ndim < 2 or x.shape[-1] != 32 or x.dtype != torch.float32 or x.device.type != "cuda"
+            or not x.is_contiguous()):
+        raise ValueError("short LayerNorm requires contiguous device float32 rows of width 32")
+    if torch.is_grad_enabled():
+        raise ValueError("short LayerNorm requires disabled gradients")
+    for name, tensor in (("weight", weight), ("bias", bias)):
+        if tensor is not None and (tensor.shape != (32,) or tensor.device != x.device
+                                   or tensor.dtype != x.dtype or not tensor.is_contiguous()):
+            raise ValueError(f"{name} must match the normalized feature dimension")
+    if weight is None:
+        raise ValueError("short LayerNorm requires affine weight")
+    return layer_norm(x, weight, bias, eps)
