@@ -401,6 +401,83 @@ def test_empty_batch_returns_empty(gpu_ready):
         assert out.shape == (0, 16, 2, 64) and out.dtype == dtype
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_left_padding_with_causal_mask(gpu_ready, dtype, head_dim):
+    # Left padding: the first keys of each sequence are masked, so under the
+    # causal bound the first rows have no allowed key (exact zeros) while
+    # later rows of the same wavefront start their running max in the same
+    # tiles.  The 16-bit kernel once rescaled those empty rows by
+    # exp2(-inf - (-inf)) = NaN when another row of the wavefront moved its
+    # reference.
+    g = torch.Generator().manual_seed(71 + head_dim)
+    batch, seq_len, heads = 3, 230, 2
+    q, k, v = (torch.randn(batch, seq_len, heads, head_dim, generator=g).to(dtype) for _ in range(3))
+    pad = torch.tensor([1, 5, 70])  # masked keys at the start of each sequence
+    mask = torch.arange(seq_len)[None, :] >= pad[:, None]
+    actual = run_hip(q, k, v, mask, True)
+    reference = oracle(q, k, v, mask, True)
+    assert bool(torch.isfinite(actual.float()).all())
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, dtype)
+    for b in range(batch):
+        assert bool((actual[b, : int(pad[b])] == 0).all())
+
+
+def _random_case(rng: torch.Generator):
+    """One randomized attention case: shapes, dtype, layout, mask and scale."""
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731
+    batch = int(torch.randint(1, 4, (1,), generator=rng))
+    seq_len = int(torch.randint(1, 301, (1,), generator=rng))
+    heads = int(torch.randint(1, 5, (1,), generator=rng))
+    head_dim = pick([8, 16, 32, 64, 128])
+    dtype = pick([torch.float32, torch.bfloat16, torch.float16])
+    causal = bool(torch.randint(2, (1,), generator=rng))
+    mask_mode = pick(["none", "prefix", "holes"])
+    layout = pick(["contiguous", "bhsd", "packed"])
+    scale = pick([None, None, 0.05, 0.3])
+    return batch, seq_len, heads, head_dim, dtype, causal, mask_mode, layout, scale
+
+
+@pytest.mark.parametrize("case_seed", range(120))
+def test_randomized_shapes_layouts_and_masks(gpu_ready, case_seed):
+    # Seeded random sweep over everything the contract admits at small sizes:
+    # head dims, dtypes, causal or not, ragged lengths, default or explicit
+    # scales, contiguous / permuted (BHSD strides) / packed-QKV layouts, and
+    # key masks as prefixes or with random holes (valid and invalid keys
+    # interleaved inside tiles).
+    rng = torch.Generator().manual_seed(1000 + case_seed)
+    batch, seq_len, heads, head_dim, dtype, causal, mask_mode, layout, scale = _random_case(rng)
+    shape = (batch, seq_len, heads, head_dim)
+    dev = torch.device("cuda")
+    if layout == "packed":
+        packed = torch.randn(batch, seq_len, 3, heads, head_dim, generator=rng).to(dtype).to(dev)
+        q, k, v = packed.unbind(dim=2)
+    elif layout == "bhsd":
+        q, k, v = (torch.randn(batch, heads, seq_len, head_dim, generator=rng).to(dtype).to(dev).transpose(1, 2)
+                   for _ in range(3))
+    else:
+        q, k, v = (torch.randn(shape, generator=rng).to(dtype).to(dev) for _ in range(3))
+    if mask_mode == "holes":
+        mask = torch.rand(batch, seq_len, generator=rng) > 0.35
+    else:
+        mask = make_mask(mask_mode, batch, seq_len)
+    actual = run_hip(q, k, v, mask, causal, scale=scale)
+    reference = oracle(q.cpu(), k.cpu(), v.cpu(), mask, causal, scale=scale)
+    label = f"case {case_seed}: {shape} {dtype} causal={causal} mask={mask_mode} layout={layout} scale={scale}"
+    assert actual.shape == shape and actual.dtype == dtype, label
+    assert contract_failures(actual, reference) == 0, label
+    if scale is None:
+        tight_check(actual, reference, dtype)
+    if mask is not None:
+        # Rows with no allowed key are exact zeros.
+        allowed = mask[:, None, :].expand(batch, seq_len, seq_len)
+        if causal:
+            allowed = allowed & torch.ones(seq_len, seq_len, dtype=torch.bool).tril()[None]
+        empty = ~allowed.any(dim=2)
+        assert bool((actual[empty] == 0).all()), label
+
+
 @pytest.mark.parametrize("seq_len", [1024, 4096])
 def test_baseline_size_rows_match_chunked_oracle(gpu_ready, seq_len):
     # BASELINE config 2 geometry (B=8, H=16, D=64, fp32); the oracle checks a

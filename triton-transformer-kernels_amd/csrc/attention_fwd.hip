@@ -882,7 +882,9 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       const bool need = (mt - m_run) * c > 8.0f;  // false for two -inf
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
         const float m_new = need ? mt : m_run;
-        const float alpha = fast_exp2((m_run - m_new) * c);  // 0 from -inf, else <= 1
+        // 1 where the reference stays (also at -inf, where the difference
+        // would be NaN), 0 from -inf, else < 1.
+        const float alpha = m_new == m_run ? 1.0f : fast_exp2((m_run - m_new) * c);
         l_run *= alpha;
 #pragma unroll
         for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
@@ -942,7 +944,10 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
             const bool need = (mt - m_run) * c > 8.0f;
             rebase_any = __builtin_amdgcn_ballot_w64(need) != 0;
             m_use = rebase_any && need ? mt : m_run;
-            alpha = fast_exp2((m_run - m_use) * c);
+            // 1 where the reference stays: a row still at -inf (no allowed
+            // key so far) must not turn its zeros into NaN when another row
+            // of the wavefront moves.
+            alpha = m_use == m_run ? 1.0f : fast_exp2((m_run - m_use) * c);
             mc = ((MASKED && m_use == -INFINITY) ? 0.0f : m_use) * c;
           }
         } else {
