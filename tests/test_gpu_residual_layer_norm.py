@@ -191,3 +191,32 @@ def test_short_layer_norm_width_32(gpu_ready, rows, bias):
     with torch.inference_mode():
         y = short_layer_norm(x.cuda(), w.cuda(), None if b is None else b.cuda(), 3e-4).cpu()
     torch.testing.assert_close(y, torch.nn.functional.layer_norm(x, (32,), w, b, 3e-4), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("case_seed", range(40))
+def test_randomized_rows_widths_masks_and_flags(gpu_ready, case_seed):
+    # Seeded random sweep: widths 1..6000 (vector and block-per-row kernels),
+    # dtypes, leading shapes, row masks with both zeroing flags, optional
+    # bias and eps.
+    rng = torch.Generator().manual_seed(300 + case_seed)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731
+    hidden = pick([1, 7, 32, 64, 96, 250, 512, 768, 1000, 1024, 2048, 4096, 6000])
+    dtype = pick([torch.float32, torch.bfloat16, torch.float16])
+    lead = pick([(3,), (2, 5), (1, 1, 7), (33,)])
+    with_bias = bool(torch.randint(2, (1,), generator=rng))
+    eps = pick([1e-5, 1e-6, 3e-4])
+    masked = bool(torch.randint(2, (1,), generator=rng))
+    zr = masked and bool(torch.randint(2, (1,), generator=rng))
+    zn = masked and bool(torch.randint(2, (1,), generator=rng))
+    x = (torch.randn(*lead, hidden, generator=rng) * 3).to(dtype)
+    u = torch.randn(x.shape, generator=rng).to(dtype)
+    w = (torch.rand(hidden, generator=rng) + 0.5).to(dtype)
+    b = (torch.randn(hidden, generator=rng) * 0.1).to(dtype) if with_bias else None
+    mask = (torch.rand(lead, generator=rng) > 0.3) if masked else None
+    er, ey = explicit_residual_layer_norm(x, u, w, b, eps, mask, zero_invalid_residual=zr,
+                                          zero_invalid_normalized=zn)
+    r, y = run_hip(x, u, w, b, eps, mask, zr, zn)
+    label = f"case {case_seed}: {tuple(x.shape)} {dtype} bias={with_bias} eps={eps} mask={masked} zr={zr} zn={zn}"
+    torch.testing.assert_close(r, er, rtol=0, atol=0, msg=label)
+    tol = {torch.float32: 1e-5, torch.bfloat16: 1.6e-2, torch.float16: 2e-3}[dtype]
+    torch.testing.assert_close(y.float(), ey.float(), rtol=tol, atol=tol, msg=label)

@@ -148,6 +148,50 @@ def test_run_accuracy_tests_harness(gpu_ready, capsys):
     assert "summary: PASS" in capsys.readouterr().out
 
 
+@pytest.mark.parametrize("case_seed", range(16))
+def test_randomized_small_models_with_left_right_and_hole_padding(gpu_ready, case_seed):
+    # Seeded random encoders (width, heads, FFN, layers, causal, dtype) with
+    # key-padding masks of three kinds: right padding (the organizer's),
+    # left padding (masked leading keys) and random holes.  fp32 against the
+    # organizer's rule on every element; bf16 / fp16 against the fp32 oracle
+    # on the rounded weights and inputs with the stated model bound; rows the
+    # mask invalidates are exact zeros.
+    rng = torch.Generator().manual_seed(900 + case_seed)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731
+    heads, head_dim = pick([(2, 32), (4, 16), (4, 64), (8, 64), (2, 128)])
+    d_model = heads * head_dim
+    batch = int(torch.randint(1, 4, (1,), generator=rng))
+    seq_len = int(torch.randint(2, 200, (1,), generator=rng))
+    layers = int(torch.randint(1, 3, (1,), generator=rng))
+    causal = bool(torch.randint(2, (1,), generator=rng))
+    dtype = pick([torch.float32, torch.float32, torch.bfloat16, torch.float16])
+    padding = pick(["right", "left", "holes"])
+    cfg = TransformerConfig(batch, seq_len, d_model, heads, 4 * d_model, layers, causal)
+    baseline, model = build(cfg, dtype=dtype, seed=case_seed)
+    if dtype != torch.float32:
+        baseline.load_state_dict({k: v.to(dtype).float() for k, v in baseline.state_dict().items()})
+    positions = torch.arange(seq_len)[None, :]
+    if padding == "holes":
+        mask = torch.rand(batch, seq_len, generator=rng) > 0.3
+    else:
+        cut = torch.randint(0, seq_len // 2 + 1, (batch, 1), generator=rng)
+        mask = positions >= cut if padding == "left" else positions < seq_len - cut
+    x = torch.randn(batch, seq_len, d_model, generator=rng).masked_fill(~mask[..., None], 0).to(dtype)
+    with torch.inference_mode():
+        ref = baseline(x.float(), mask)
+        out = model(x.cuda(), mask.cuda()).float().cpu()
+    label = f"case {case_seed}: {cfg} {dtype} padding={padding}"
+    assert bool(torch.isfinite(out).all()), label
+    assert bool((out[~mask] == 0).all()), label
+    if dtype == torch.float32:
+        res = compare_outputs(ref, out, rtol=0.01, atol=0.001)
+        assert res.passed, f"{label}: failed={res.failed_elements} max_abs={res.max_abs_error:.3e}"
+    else:
+        err = (out - ref).abs()
+        ok = (err <= 5e-2) | (err <= 0.05 * ref.abs())
+        assert bool(ok.all()), f"{label}: failed={int((~ok).sum())} max_abs={err.max().item():.3g}"
+
+
 def test_explicit_all_valid_mask_matches_no_mask(gpu_ready):
     cfg = TransformerConfig(2, 33, 64, 4, 128, 1, True)
     _, model = build(cfg, execution_mode="eager")
