@@ -424,6 +424,32 @@ def test_left_padding_with_causal_mask(gpu_ready, dtype, head_dim):
         assert bool((actual[b, : int(pad[b])] == 0).all())
 
 
+@pytest.mark.parametrize("head_dim", [64, 32])
+def test_paired_grid_with_key_masks(gpu_ready, head_dim):
+    # The fp32 paired schedule (a workgroup runs query tiles nq-1-i and i) is
+    # chosen only for grids that fill every workgroup slot, e.g. the config-2
+    # shape B=8, S=1024, H=16; together with the diagonal hand-off and the
+    # priority alternation it is checked here under key masks: left padding
+    # of varying length (rows with no allowed key) and random holes.  Three
+    # heads of every batch element are compared with the oracle.
+    g = torch.Generator().manual_seed(91 + head_dim)
+    batch, seq_len, heads = 8, 1024, 16
+    q, k, v = (torch.randn(batch, seq_len, heads, head_dim, generator=g) for _ in range(3))
+    positions = torch.arange(seq_len)[None, :]
+    pad = torch.tensor([0, 1, 3, 40, 100, 130, 0, 500])[:, None]
+    mask = positions >= pad
+    mask[6] &= torch.rand(seq_len, generator=g) > 0.3  # holes
+    mask[7] &= torch.rand(seq_len, generator=g) > 0.5
+    actual = run_hip(q, k, v, mask, True)
+    for hh in (0, 7, 15):
+        sl = slice(hh, hh + 1)
+        reference = oracle(q[:, :, sl], k[:, :, sl], v[:, :, sl], mask, True)
+        assert contract_failures(actual[:, :, sl], reference) == 0, f"head {hh}"
+        tight_check(actual[:, :, sl], reference, torch.float32)
+    for b in range(batch):
+        assert bool((actual[b, : int(pad[b])] == 0).all())
+
+
 def _random_case(rng: torch.Generator, max_len: int = 300):
     """One randomized attention case: shapes, dtype, layout, mask and scale."""
     pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731
