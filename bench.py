@@ -226,6 +226,8 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
     attention:      fp32 causal [8,S,16,64], S = --seq-len (1024: the headline step)
     attention_bf16: bf16 causal [1,16384,32,128] (config 5a)
     attention_bf16_d64: bf16 causal [4,2048,16,64] (the attention of the config-4 encoder)
+    attention_5b:   fp32 non-causal [512,64,8,64] on packed-QKV views (the attention of the
+                    config-5b encoder)
     encoder_fp32 / encoder_bf16: config-4 encoder forward (hipGraph replay), for the
                     per-kernel split
     encoder_5b:     config-5b encoder forward (fp32, B=512, S=64, d=512, 4 layers,
@@ -257,6 +259,13 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         out = torch.empty_like(q)
         fn = lambda: hip_attention(q, k, v, causal=True, out=out)  # noqa: E731
         work = attention_flops(4, 16, 2048, 64, True)
+    elif which == "attention_5b":
+        g = torch.Generator(device="cuda").manual_seed(7)
+        packed = torch.randn(512, 64, 3, 8, 64, device="cuda", generator=g)
+        q, k, v = packed.unbind(dim=2)
+        out = torch.empty(512, 64, 8, 64, device="cuda")
+        fn = lambda: hip_attention(q, k, v, causal=False, out=out)  # noqa: E731
+        work = attention_flops(512, 8, 64, 64, False)
     elif which == "layernorm":
         rows = 32768
         nsets = max(1, -(-2 * MALL_BYTES // (rows * hidden * 4 * 4)))
@@ -349,7 +358,7 @@ def main() -> int:
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16",
-                                                   "attention_bf16_d64", "encoder_fp32", "encoder_bf16",
+                                                   "attention_bf16_d64", "attention_5b", "encoder_fp32", "encoder_bf16",
                                                    "encoder_5b", "linear_gelu", "gelu"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,

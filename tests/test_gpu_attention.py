@@ -450,6 +450,66 @@ def test_paired_grid_with_key_masks(gpu_ready, head_dim):
         assert bool((actual[b, : int(pad[b])] == 0).all())
 
 
+def _layout_inputs(shape, layout: str, rng: torch.Generator, dtype=torch.float32):
+    """q, k, v on the GPU as contiguous BSHD, permuted BHSD views or packed-QKV views."""
+    batch, seq_len, heads, head_dim = shape
+    dev = torch.device("cuda")
+    if layout == "packed":
+        packed = torch.randn(batch, seq_len, 3, heads, head_dim, generator=rng).to(dtype).to(dev)
+        return packed.unbind(dim=2)
+    if layout == "bhsd":
+        return tuple(torch.randn(batch, heads, seq_len, head_dim, generator=rng).to(dtype).to(dev).transpose(1, 2)
+                     for _ in range(3))
+    return tuple(torch.randn(shape, generator=rng).to(dtype).to(dev) for _ in range(3))
+
+
+@pytest.mark.parametrize("batch,seq_len,heads,head_dim,mask_mode,layout", [
+    (3, 64, 3, 64, "holes", "contiguous"),  # B*H = 9: the last workgroup has one pair
+    (1, 1, 1, 64, "none", "contiguous"),
+    (2, 33, 5, 32, "prefix", "bhsd"),
+    (5, 17, 1, 16, "holes", "packed"),
+    (4, 64, 2, 8, "none", "packed"),
+    (1, 64, 7, 64, "prefix", "bhsd"),
+    (2, 32, 3, 64, "holes", "contiguous"),
+])
+def test_twin_grid_short_sequences(gpu_ready, batch, seq_len, heads, head_dim, mask_mode, layout):
+    # fp32 non-causal attention with S <= 64 (one key tile; a 128-query tile
+    # has rows for two of its four wavefronts) runs two (batch, head) pairs
+    # per workgroup, wavefronts 0-1 on pair 2i and 2-3 on pair 2i + 1, each
+    # pair's keys in its own LDS buffer.  Odd B*H leaves the second pair of
+    # the last workgroup empty.  Every head is compared with the oracle.
+    rng = torch.Generator().manual_seed(batch * 1000 + seq_len * 10 + heads + head_dim)
+    q, k, v = _layout_inputs((batch, seq_len, heads, head_dim), layout, rng)
+    if mask_mode == "holes":
+        mask = torch.rand(batch, seq_len, generator=rng) > 0.4
+        mask[0, :] = False  # one batch element with no valid key: zero rows
+    else:
+        mask = make_mask(mask_mode, batch, seq_len)
+    for scale in (None, 0.3):
+        actual = run_hip(q, k, v, mask, False, scale)
+        reference = oracle(q.cpu(), k.cpu(), v.cpu(), mask, False, scale)
+        assert contract_failures(actual, reference) == 0, f"scale={scale}"
+        tight_check(actual, reference, torch.float32)
+    if mask_mode == "holes":
+        assert bool((actual[0] == 0).all())
+
+
+def test_twin_grid_config5b_shape_with_padding(gpu_ready):
+    # Config 5b's attention (fp32, B=512, S=64, H=8, D=64, non-causal) with
+    # right padding of every length 1..64 and random holes, every head
+    # against the oracle.
+    rng = torch.Generator().manual_seed(55)
+    batch, seq_len, heads, head_dim = 512, 64, 8, 64
+    q, k, v = _layout_inputs((batch, seq_len, heads, head_dim), "packed", rng)
+    lengths = torch.arange(batch) % seq_len + 1
+    mask = torch.arange(seq_len)[None, :] < lengths[:, None]
+    mask[::7] &= torch.rand(mask[::7].shape, generator=rng) > 0.25
+    actual = run_hip(q, k, v, mask, False)
+    reference = oracle(q.cpu(), k.cpu(), v.cpu(), mask, False)
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, torch.float32)
+
+
 def _random_case(rng: torch.Generator, max_len: int = 300):
     """One randomized attention case: shapes, dtype, layout, mask and scale."""
     pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731

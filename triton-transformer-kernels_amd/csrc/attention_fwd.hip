@@ -266,8 +266,19 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   const int h = lane >> 5;
 
   const Work w = work_item(p, CAUSAL);
-  const int b = w.bh / p.H;
-  const int hh = w.bh - b * p.H;
+  // Twin grid (S <= 64, one key tile, rows only for wavefronts 0-1 of a
+  // 128-query tile): workgroup i serves (batch, head) pairs 2i (wavefronts
+  // 0-1, K/V buffer 0) and 2i + 1 (wavefronts 2-3, buffer 1).  The second
+  // pair of the last workgroup may not exist (odd B*H): its wavefronts hold
+  // no rows and read nothing.  Built into the non-causal kernels only (the
+  // causal ones keep their register budget for the pairing and hand-off).
+  constexpr bool kTwin = !CAUSAL && BN == 64;
+  const bool twin = kTwin && p.twin != 0;
+  const int slot = twin ? (wave >> 1) : 0;
+  const int bh = twin ? 2 * static_cast<int>(blockIdx.x) + slot : w.bh;
+  const bool head_live = bh < p.BH;
+  const int b = head_live ? bh / p.H : 0;
+  const int hh = head_live ? bh - b * p.H : 0;
   const int S = p.S;
   const float* __restrict__ Q = static_cast<const float*>(p.q) + b * p.qb + hh * p.qh;
   const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.kb + hh * p.kh;
@@ -290,7 +301,9 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   int tiles_done = 0;
   for (int pass = 0; pass < w.npass; ++pass) {
     const int qb = pass == 0 ? w.q_first : w.q_second;
-    const int q0 = qb * kBM + wave * 32;  // first query of this wavefront (uniform)
+    // First query of this wavefront (uniform); S, i.e. no rows, for the
+    // missing second pair of a twin workgroup.
+    const int q0 = !head_live ? S : qb * kBM + (twin ? (wave & 1) : wave) * 32;
     int qrow = q0 + m;                    // query of this lane (wavefront 3's on a hand-off)
 
     // B operand of S^T = K.Q^T: group g covers d = 8g..8g+7, lane half h
@@ -500,13 +513,65 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       }
     };
 
-    if (!staged) gload(0);
-    uint64_t kvalid = lstore(0, 0);
+    // Twin grid: both pairs' only key tile, pair 2i into buffer 0 and 2i + 1
+    // into buffer 1, every load issued before the first LDS store; returns
+    // this wavefront's valid-key bits.
+    auto twin_stage = [&]() -> uint64_t {
+      f32x4 tk[2][CPT], tv[2][CPT];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int bhx = 2 * static_cast<int>(blockIdx.x) + s2;
+        const bool live = bhx < p.BH;
+        const int bx = live ? bhx / p.H : 0;
+        const int hx = live ? bhx - bx * p.H : 0;
+        const float* Kx = static_cast<const float*>(p.k) + bx * p.kb + hx * p.kh;
+        const float* Vx = static_cast<const float*>(p.v) + bx * p.vb + hx * p.vh;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const int idx = tid + kThreads * i;
+          if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
+            const int row = idx / CPR;  // key: the tile starts at key 0
+            const int c = idx - row * CPR;
+            if (live && row < S) {
+              tk[s2][i] = *reinterpret_cast<const f32x4*>(Kx + row * p.ks + 4 * c);
+              tv[s2][i] = *reinterpret_cast<const f32x4*>(Vx + row * p.vs + 4 * c);
+            } else {
+              tk[s2][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+              tv[s2][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+          }
+        }
+      }
+      bool valid = head_live && lane < S;
+      if constexpr (HAS_MASK) valid = valid && M[lane * p.ms] != 0;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const int idx = tid + kThreads * i;
+          if (C::CHUNKS % kThreads == 0 || idx < C::CHUNKS) {
+            const int row = idx / CPR;
+            const int c = idx - row * CPR;
+            *reinterpret_cast<f32x4*>(&smK[s2][row * KS + 4 * c]) = tk[s2][i];
+            *reinterpret_cast<f32x4*>(&smV[s2][row * D + 4 * c]) = tv[s2][i];
+          }
+        }
+      }
+      return HAS_MASK ? __builtin_amdgcn_ballot_w64(valid) : range_bits(0, S);
+    };
+
+    uint64_t kvalid;
+    if (kTwin && twin) {
+      kvalid = twin_stage();
+    } else {
+      if (!staged) gload(0);
+      kvalid = lstore(0, 0);
+    }
     __syncthreads();
     staged = false;
 
     for (int t = 0; t < ntiles; ++t) {
-      const int buf = t & 1;
+      const int buf = twin ? slot : (t & 1);
       if (((tiles_done + t) & 1) == prio_phase) {
         __builtin_amdgcn_s_setprio(1);
       } else {
@@ -1104,7 +1169,12 @@ hipError_t launch_d(int dtype, AttnParams& p, hipStream_t stream) {
             paired >= static_cast<int64_t>(device_cu_count()) * kMinWaves<true, D>) ? 1 : 0;
   p.units = p.pair ? (p.nq + 1) / 2 : p.nq;
   p.cu_count = device_cu_count();
-  const dim3 g(static_cast<unsigned>(p.units) * static_cast<unsigned>(p.BH)), blk(kThreads);
+  // One 64-key tile per head and rows for wavefronts 0-1 only: two heads per
+  // workgroup (fp32 non-causal kernels, whose second K/V buffer is free).
+  p.twin = (dtype == 0 && !CAUSAL && F32Cfg<D>::BN == 64 && p.S <= 64) ? 1 : 0;
+  const unsigned groups = p.twin ? static_cast<unsigned>((p.BH + 1) / 2)
+                                 : static_cast<unsigned>(p.units) * static_cast<unsigned>(p.BH);
+  const dim3 g(groups), blk(kThreads);
   switch (dtype) {
     case 0: attn_fwd_f32_kernel<D, CAUSAL, HAS_MASK><<<g, blk, 0, stream>>>(p); break;
     case 1: attn_fwd_h16_kernel<BF16, D, CAUSAL, HAS_MASK><<<g, blk, 0, stream>>>(p); break;

@@ -93,6 +93,7 @@ struct AttnParams {
   int pair;          // causal: a workgroup runs query tiles nq-1-i and i
   int units;         // workgroups per (batch, head)
   int cu_count;      // compute units of the device (wave-priority phase)
+  int twin;          // fp32, S <= 64: two (batch, head) pairs per workgroup
 };
 
 // Launch parameters of the residual + LayerNorm kernels.
