@@ -237,6 +237,8 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
     gelu:           exact GELU, bf16, the config-4 FFN activation [8192, 4096] (GB/s)
     layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
                     among input sets that together exceed twice the 256 MB MALL
+    layernorm_bf16: bf16 residual+LN rows=8192, hidden=1024 (the config-4 encoder's LN),
+                    rotating input sets as above
     copy:           a plain device copy of 256 MiB (the PMC byte-counter calibration:
                     FETCH_SIZE and WRITE_SIZE should each read 262144 KiB per dispatch)
     """
@@ -280,6 +282,20 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
             fused_residual_layer_norm(x, u, w, b, 1e-5)
 
         work = layer_norm_bytes(rows, hidden)
+    elif which == "layernorm_bf16":
+        rows, width = 8192, 1024
+        nsets = max(1, -(-2 * MALL_BYTES // (rows * width * 2 * 4)))
+        sets = [(torch.randn(rows, width, device="cuda").to(torch.bfloat16),
+                 torch.randn(rows, width, device="cuda").to(torch.bfloat16)) for _ in range(nsets)]
+        w = (torch.rand(width, device="cuda") + 0.5).to(torch.bfloat16)
+        b = (torch.randn(width, device="cuda") * 0.1).to(torch.bfloat16)
+        calls = iter(range(1 << 62))
+
+        def fn():
+            x, u = sets[next(calls) % nsets]
+            fused_residual_layer_norm(x, u, w, b, 1e-5)
+
+        work = layer_norm_bytes(rows, width, elem=2)
     elif which == "linear_gelu":
         from transformer_opt.kernels import linear_gelu
 
@@ -329,7 +345,7 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         finish.record()
         torch.cuda.synchronize()
     ms = begin.elapsed_time(finish) / steps
-    if which in ("layernorm", "copy", "gelu"):
+    if which in ("layernorm", "layernorm_bf16", "copy", "gelu"):
         rate, unit = work / (ms * 1e-3) / 1e9, "GB/s"
     elif which.startswith("encoder"):
         rate, unit = work / (ms * 1e-3), "tokens/s"
@@ -357,7 +373,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=50)
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--profile-only", choices=("attention", "layernorm", "copy", "attention_bf16",
+    parser.add_argument("--profile-only", choices=("attention", "layernorm", "layernorm_bf16", "copy", "attention_bf16",
                                                    "attention_bf16_d64", "attention_5b", "encoder_fp32", "encoder_bf16",
                                                    "encoder_5b", "linear_gelu", "gelu"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
