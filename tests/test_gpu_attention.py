@@ -450,6 +450,33 @@ def test_paired_grid_with_key_masks(gpu_ready, head_dim):
         assert bool((actual[b, : int(pad[b])] == 0).all())
 
 
+@pytest.mark.parametrize("batch,seq_len,heads,head_dim,mask_mode", [
+    (8, 512, 16, 64, "holes"),   # config 2 at S=512: 4 query tiles x 128 heads = 512 workgroups
+    (3, 400, 32, 64, "prefix"),  # 384 workgroups, ragged last tile
+    (2, 700, 24, 32, "none"),    # 6 query tiles x 48 heads = 288 workgroups
+])
+def test_folded_grid_one_round(gpu_ready, batch, seq_len, heads, head_dim, mask_mode):
+    # An unpaired causal fp32 grid that is resident in one round (more
+    # workgroups than CUs, at most two per CU) runs its query tiles in folded
+    # order - heavy tiles descending, then light tiles ascending - so the two
+    # workgroups of a CU carry tiles of opposite weight.  Every head is
+    # compared with the oracle.
+    rng = torch.Generator().manual_seed(seq_len + heads)
+    shape = (batch, seq_len, heads, head_dim)
+    q, k, v = (torch.randn(shape, generator=rng) for _ in range(3))
+    if mask_mode == "holes":
+        mask = torch.rand(batch, seq_len, generator=rng) > 0.3
+        mask[1, :200] = False  # left padding: rows with no allowed key
+    else:
+        mask = make_mask(mask_mode, batch, seq_len)
+    actual = run_hip(q, k, v, mask, True)
+    reference = oracle(q, k, v, mask, True)
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, torch.float32)
+    if mask_mode == "holes":
+        assert bool((actual[1, :200] == 0).all())
+
+
 def _layout_inputs(shape, layout: str, rng: torch.Generator, dtype=torch.float32):
     """q, k, v on the GPU as contiguous BSHD, permuted BHSD views or packed-QKV views."""
     batch, seq_len, heads, head_dim = shape

@@ -94,6 +94,7 @@ struct AttnParams {
   int units;         // workgroups per (batch, head)
   int cu_count;      // compute units of the device (wave-priority phase)
   int twin;          // fp32, S <= 64: two (batch, head) pairs per workgroup
+  int fold;          // causal, one resident round: heavy/light query-tile order
 };
 
 // Launch parameters of the residual + LayerNorm kernels.
