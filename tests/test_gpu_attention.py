@@ -454,6 +454,7 @@ def test_paired_grid_with_key_masks(gpu_ready, head_dim):
     (8, 512, 16, 64, "holes"),   # config 2 at S=512: 4 query tiles x 128 heads = 512 workgroups
     (3, 400, 32, 64, "prefix"),  # 384 workgroups, ragged last tile
     (2, 700, 24, 32, "none"),    # 6 query tiles x 48 heads = 288 workgroups
+    (5, 600, 13, 64, "holes"),   # B*H = 65: no XCD swizzle; 5 query tiles, 325 workgroups
 ])
 def test_folded_grid_one_round(gpu_ready, batch, seq_len, heads, head_dim, mask_mode):
     # An unpaired causal fp32 grid that is resident in one round (more
