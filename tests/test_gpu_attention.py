@@ -195,7 +195,7 @@ def test_all_keys_masked_is_finite_zero(gpu_ready):
 
 
 @pytest.mark.parametrize("seq_len", [31, 32, 33, 63, 64, 65, 127, 128, 129, 257])
-@pytest.mark.parametrize("head_dim", [32, 128])
+@pytest.mark.parametrize("head_dim", [16, 32, 128])
 @pytest.mark.parametrize("mask_mode", ["none", "minimum"])
 def test_causal_frontier_matches_reference_at_tile_boundaries(gpu_ready, seq_len, head_dim, mask_mode):
     # Reference tests/test_gpu_attention.py:153-169.
@@ -210,7 +210,7 @@ def test_causal_frontier_matches_reference_at_tile_boundaries(gpu_ready, seq_len
 
 
 @pytest.mark.parametrize("seq_len", [97, 127, 128, 225, 353, 384])
-@pytest.mark.parametrize("head_dim", [8, 32, 64])
+@pytest.mark.parametrize("head_dim", [8, 16, 32, 64])
 @pytest.mark.parametrize("mask_mode", ["none", "drop_last32", "only_last32"])
 def test_causal_last_diagonal_sub_block_split_between_wavefronts(gpu_ready, seq_len, head_dim, mask_mode):
     # fp32 causal: in the last key tile of a 128-query tile, the keys
@@ -424,7 +424,7 @@ def test_left_padding_with_causal_mask(gpu_ready, dtype, head_dim):
         assert bool((actual[b, : int(pad[b])] == 0).all())
 
 
-@pytest.mark.parametrize("head_dim", [64, 32])
+@pytest.mark.parametrize("head_dim", [64, 32, 16])
 def test_paired_grid_with_key_masks(gpu_ready, head_dim):
     # The fp32 paired schedule (a workgroup runs query tiles nq-1-i and i) is
     # chosen only for grids that fill every workgroup slot, e.g. the config-2
@@ -455,6 +455,7 @@ def test_paired_grid_with_key_masks(gpu_ready, head_dim):
     (3, 400, 32, 64, "prefix"),  # 384 workgroups, ragged last tile
     (2, 700, 24, 32, "none"),    # 6 query tiles x 48 heads = 288 workgroups
     (5, 600, 13, 64, "holes"),   # B*H = 65: no XCD swizzle; 5 query tiles, 325 workgroups
+    (4, 500, 32, 16, "holes"),   # head_dim 16 (16x16x4 P.V): 4 query tiles x 128 heads
 ])
 def test_folded_grid_one_round(gpu_ready, batch, seq_len, heads, head_dim, mask_mode):
     # An unpaired causal fp32 grid that is resident in one round (more

@@ -115,6 +115,22 @@ __device__ __forceinline__ float sum_with_other_half(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Per-query value (32x32 result layout: query l % 32, equal in both lane
+// halves) re-read for the 16x16 output layout through v_permlane16_swap of
+// (x, x), which swaps the odd 16-lane rows of the first operand with the even
+// rows of the second: lo = the value of query l % 16, hi = that of query
+// 16 + l % 16.
+__device__ __forceinline__ void by_query16(float x, float& lo, float& hi) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ f32x4 mfma_f32_16(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 // LDS-DMA: each active lane copies the 16 bytes at gbase + voff (gbase
 // wave-uniform, voff the lane's byte offset) to lds_base + 16 * lane
 // (global_load_lds_dwordx4; lds_base is wave-uniform).  Completion is tracked
@@ -264,6 +280,9 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   // 16*DB accumulator values, the row max and the lane half's row sum, as
   // 16-byte chunks at smX[(chunk * 64 + lane) * 4].
   constexpr bool kHandoff = CAUSAL && NSB == 2;
+  // head_dim 16: P.V on 16x16x4 MFMAs (a 32x32 block would leave half its
+  // rows empty); the accumulator keeps the f32x16 storage, elements 0-7 used.
+  constexpr bool kD16 = D == 16;
   constexpr int NX4 = 4 * DB + 1;
   __shared__ __attribute__((aligned(16))) float smX[kHandoff ? NX4 * 256 : 4];
 
@@ -466,10 +485,53 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
           ls += pr;
         }
       l_run = __builtin_fmaf(l_run, alpha, ls);
+      if constexpr (kD16) {
+        float a_lo, a_hi;
+        by_query16(alpha, a_lo, a_hi);
 #pragma unroll
-      for (int i = 0; i < DB; ++i) acc[i] *= alpha;
+        for (int e = 0; e < 4; ++e) {
+          acc[0][e] *= a_lo;
+          acc[0][4 + e] *= a_hi;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < DB; ++i) acc[i] *= alpha;
+      }
       m_run = m_new;
       fence();
+      if constexpr (kD16) {
+        // ---- head_dim 16: O^T += V^T . P^T on 16x16x4 MFMAs ---------------
+        // v_permlane16_swap of score registers r, r + 1 (keys k, k + 1 in lane
+        // half 0, k + 4, k + 5 in half 1, k = 8(r/4) + r%4) leaves queries
+        // 0-15 in the first and 16-31 in the second, with key k + {0,1,4,5}[g]
+        // in 16-lane row g: the B operands of the two 16-query output blocks,
+        // sharing one A operand V[key][d = l % 16].  Accumulator elements
+        // 0-3 hold block 0 (d = 4(l/16) + e, query l % 16), 4-7 block 1.
+        const int g16 = lane >> 4;
+        const int vkey = (g16 & 1) + 4 * (g16 >> 1);
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          if (PARTIAL && sb >= nlive) continue;
+          const float* vb = &smV[buf][((SB0 + sb) * 32 + vkey) * D + (lane & 15)];
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const float va = vb[(8 * (r >> 2) + (r & 3)) * D];
+            const auto pq = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[sb][r]),
+                                                             __float_as_uint(s[sb][r + 1]), false, false);
+            f32x4 lo = {acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+            f32x4 hi = {acc[0][4], acc[0][5], acc[0][6], acc[0][7]};
+            lo = mfma_f32_16(va, __uint_as_float(pq[0]), lo);
+            hi = mfma_f32_16(va, __uint_as_float(pq[1]), hi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              acc[0][e] = lo[e];
+              acc[0][4 + e] = hi[e];
+            }
+          }
+        }
+        fence();
+        return;
+      }
       // ---- O^T += V^T . P^T (V fragments read one k-step ahead) -----------
       const int nsteps = (PARTIAL ? nlive : NSB) * 16;
       VF vf = vread(buf, SB0, 0);
@@ -503,6 +565,24 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
     // O = acc / l for this lane's row.
     auto epilogue = [&]() __attribute__((always_inline)) {
       const float lt = sum_with_other_half(l_run);
+      if constexpr (kD16) {
+        // Block 0: query base + l % 16, block 1: base + 16 + l % 16; d = 4(l/16) + e.
+        float lt_lo, lt_hi;
+        by_query16(lt, lt_lo, lt_hi);
+        const float inv_lo = lt_lo > 0.0f ? 1.0f / lt_lo : 0.0f;
+        const float inv_hi = lt_hi > 0.0f ? 1.0f / lt_hi : 0.0f;
+        const int base = qrow - m;  // first query of the rows held (uniform)
+        const int d0 = 4 * (lane >> 4);
+        float* __restrict__ O = static_cast<float*>(p.out) + b * p.ob + hh * p.oh + d0;
+        const int r_lo = base + (lane & 15), r_hi = r_lo + 16;
+        if (r_lo < S)
+          *reinterpret_cast<f32x4*>(O + r_lo * p.os) =
+              f32x4{acc[0][0] * inv_lo, acc[0][1] * inv_lo, acc[0][2] * inv_lo, acc[0][3] * inv_lo};
+        if (r_hi < S)
+          *reinterpret_cast<f32x4*>(O + r_hi * p.os) =
+              f32x4{acc[0][4] * inv_hi, acc[0][5] * inv_hi, acc[0][6] * inv_hi, acc[0][7] * inv_hi};
+        return;
+      }
       const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
       if (qrow < S) {
         float* __restrict__ O = static_cast<float*>(p.out) + b * p.ob + hh * p.oh + qrow * p.os;
@@ -670,12 +750,26 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
         const float a = fast_exp2(m_run - mu);
         const float bb = fast_exp2(ml[0] - mu);
         l_run = __builtin_fmaf(l_run, a, ml[1] * bb);
+        if constexpr (kD16) {
+          // Factors per output block (queries l % 16 and 16 + l % 16).
+          float a_lo, a_hi, b_lo, b_hi;
+          by_query16(a, a_lo, a_hi);
+          by_query16(bb, b_lo, b_hi);
 #pragma unroll
-        for (int j = 0; j < 4 * DB; ++j) {
-          const int i = j >> 2, r0 = 4 * (j & 3);
-          const f32x4 x = *reinterpret_cast<const f32x4*>(&smX[(j * 64 + lane) * 4]);
+          for (int j = 0; j < 2; ++j) {
+            const float fa = j == 0 ? a_lo : a_hi, fb = j == 0 ? b_lo : b_hi;
+            const f32x4 x = *reinterpret_cast<const f32x4*>(&smX[(j * 64 + lane) * 4]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[i][r0 + e] = __builtin_fmaf(acc[i][r0 + e], a, x[e] * bb);
+            for (int e = 0; e < 4; ++e) acc[0][4 * j + e] = __builtin_fmaf(acc[0][4 * j + e], fa, x[e] * fb);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4 * DB; ++j) {
+            const int i = j >> 2, r0 = 4 * (j & 3);
+            const f32x4 x = *reinterpret_cast<const f32x4*>(&smX[(j * 64 + lane) * 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][r0 + e] = __builtin_fmaf(acc[i][r0 + e], a, x[e] * bb);
+          }
         }
         m_run = mx;
       }
