@@ -195,7 +195,7 @@ def test_all_keys_masked_is_finite_zero(gpu_ready):
 
 
 @pytest.mark.parametrize("seq_len", [31, 32, 33, 63, 64, 65, 127, 128, 129, 257])
-@pytest.mark.parametrize("head_dim", [16, 32, 128])
+@pytest.mark.parametrize("head_dim", [8, 16, 32, 128])
 @pytest.mark.parametrize("mask_mode", ["none", "minimum"])
 def test_causal_frontier_matches_reference_at_tile_boundaries(gpu_ready, seq_len, head_dim, mask_mode):
     # Reference tests/test_gpu_attention.py:153-169.
@@ -424,7 +424,7 @@ def test_left_padding_with_causal_mask(gpu_ready, dtype, head_dim):
         assert bool((actual[b, : int(pad[b])] == 0).all())
 
 
-@pytest.mark.parametrize("head_dim", [64, 32, 16])
+@pytest.mark.parametrize("head_dim", [64, 32, 16, 8])
 def test_paired_grid_with_key_masks(gpu_ready, head_dim):
     # The fp32 paired schedule (a workgroup runs query tiles nq-1-i and i) is
     # chosen only for grids that fill every workgroup slot, e.g. the config-2

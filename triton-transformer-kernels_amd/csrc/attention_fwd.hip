@@ -280,9 +280,10 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   // 16*DB accumulator values, the row max and the lane half's row sum, as
   // 16-byte chunks at smX[(chunk * 64 + lane) * 4].
   constexpr bool kHandoff = CAUSAL && NSB == 2;
-  // head_dim 16: P.V on 16x16x4 MFMAs (a 32x32 block would leave half its
-  // rows empty); the accumulator keeps the f32x16 storage, elements 0-7 used.
-  constexpr bool kD16 = D == 16;
+  // head_dim 8 and 16: P.V on 16x16x4 MFMAs (a 32x32 block would leave 3/4 or
+  // half of its rows empty); the accumulator keeps the f32x16 storage,
+  // elements 0-7 used.
+  constexpr bool kD16 = D <= 16;
   constexpr int NX4 = 4 * DB + 1;
   __shared__ __attribute__((aligned(16))) float smX[kHandoff ? NX4 * 256 : 4];
 
@@ -500,22 +501,24 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       m_run = m_new;
       fence();
       if constexpr (kD16) {
-        // ---- head_dim 16: O^T += V^T . P^T on 16x16x4 MFMAs ---------------
+        // ---- head_dim <= 16: O^T += V^T . P^T on 16x16x4 MFMAs ------------
         // v_permlane16_swap of score registers r, r + 1 (keys k, k + 1 in lane
         // half 0, k + 4, k + 5 in half 1, k = 8(r/4) + r%4) leaves queries
         // 0-15 in the first and 16-31 in the second, with key k + {0,1,4,5}[g]
         // in 16-lane row g: the B operands of the two 16-query output blocks,
         // sharing one A operand V[key][d = l % 16].  Accumulator elements
-        // 0-3 hold block 0 (d = 4(l/16) + e, query l % 16), 4-7 block 1.
+        // 0-3 hold block 0 (d = 4(l/16) + e, query l % 16), 4-7 block 1;
+        // for head_dim 8 the rows d >= 8 multiply zeros.
         const int g16 = lane >> 4;
         const int vkey = (g16 & 1) + 4 * (g16 >> 1);
+        const bool d_ok = (lane & 15) < D;
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb) {
           if (PARTIAL && sb >= nlive) continue;
-          const float* vb = &smV[buf][((SB0 + sb) * 32 + vkey) * D + (lane & 15)];
+          const float* vb = &smV[buf][((SB0 + sb) * 32 + vkey) * D + (lane & 15 & (D - 1))];
 #pragma unroll
           for (int r = 0; r < 16; r += 2) {
-            const float va = vb[(8 * (r >> 2) + (r & 3)) * D];
+            const float va = d_ok ? vb[(8 * (r >> 2) + (r & 3)) * D] : 0.0f;
             const auto pq = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[sb][r]),
                                                              __float_as_uint(s[sb][r + 1]), false, false);
             f32x4 lo = {acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
@@ -575,6 +578,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
         const int d0 = 4 * (lane >> 4);
         float* __restrict__ O = static_cast<float*>(p.out) + b * p.ob + hh * p.oh + d0;
         const int r_lo = base + (lane & 15), r_hi = r_lo + 16;
+        if (d0 >= D) return;  // head_dim 8: d-rows 8-15 are empty
         if (r_lo < S)
           *reinterpret_cast<f32x4*>(O + r_lo * p.os) =
               f32x4{acc[0][0] * inv_lo, acc[0][1] * inv_lo, acc[0][2] * inv_lo, acc[0][3] * inv_lo};
