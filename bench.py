@@ -504,8 +504,8 @@ def main() -> int:
         log(f"residual+LN hidden=32 rows=4194304: {gbps:.0f} GB/s")
         torch.cuda.empty_cache()
         small = {}
-        for d_head, dt, name in ((8, torch.float16, "fp16"), (16, torch.float32, "fp32"),
-                                 (32, torch.float32, "fp32")):
+        for d_head, dt, name in ((8, torch.float16, "fp16"), (8, torch.float32, "fp32"),
+                                 (16, torch.float32, "fp32"), (32, torch.float32, "fp32")):
             tf, ms = attention_tflops(8, 1024, 16, d_head, True, dt)
             small[f"D{d_head}_{name}"] = {"tflops": round(tf, 2), "ms": round(ms, 4)}
             log(f"attention {name} causal [8,1024,16,{d_head}]: {tf:.1f} TF")
