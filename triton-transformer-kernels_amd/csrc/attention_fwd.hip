@@ -46,11 +46,17 @@
 //   (whose rows are complete) takes wavefront 3's diagonal sub-block and
 //   hands its partial softmax state over through LDS, so the diagonal costs
 //   3 sub-block times instead of 4.
+// * fp32 head_dim 8 and 16: P.V runs on 16x16x4 MFMAs (a 32x32 O^T block
+//   would leave 3/4 or half of its d-rows empty); v_permlane16_swap of two
+//   score registers regroups them by 16 queries, see the tile body.
 // * Scheduling: causal query tile i costs i+1 key blocks.  When the grid
 //   still fills every workgroup slot of the GPU, a workgroup runs the query
 //   tiles nq-1-i and i one after the other, so all workgroups carry the same
 //   nq+1 blocks of work and the launch has no tail.  Otherwise the flat grid
-//   is ordered heaviest query tile first.  When B*H is a multiple of 8 all
+//   is ordered heaviest query tile first, or, for an fp32 grid resident in
+//   one round, folded so that the two workgroups of a CU hold a heavy and a
+//   light tile.  fp32 non-causal with S <= 64 runs two (batch, head) pairs
+//   per workgroup (the twin grid).  When B*H is a multiple of 8 all
 //   workgroups of one head run on the same XCD (workgroups are dealt
 //   round-robin to the 8 XCDs), so a head's K/V is fetched from HBM into one
 //   XCD's L2 instead of eight.  The fp32 kernel alternates wave priority per
@@ -283,7 +289,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
   // head_dim 8 and 16: P.V on 16x16x4 MFMAs (a 32x32 block would leave 3/4 or
   // half of its rows empty); the accumulator keeps the f32x16 storage,
   // elements 0-7 used.
-  constexpr bool kD16 = D <= 16;
+  constexpr bool kNarrowD = D <= 16;
   constexpr int NX4 = 4 * DB + 1;
   __shared__ __attribute__((aligned(16))) float smX[kHandoff ? NX4 * 256 : 4];
 
@@ -486,7 +492,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
           ls += pr;
         }
       l_run = __builtin_fmaf(l_run, alpha, ls);
-      if constexpr (kD16) {
+      if constexpr (kNarrowD) {
         float a_lo, a_hi;
         by_query16(alpha, a_lo, a_hi);
 #pragma unroll
@@ -500,7 +506,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       }
       m_run = m_new;
       fence();
-      if constexpr (kD16) {
+      if constexpr (kNarrowD) {
         // ---- head_dim <= 16: O^T += V^T . P^T on 16x16x4 MFMAs ------------
         // v_permlane16_swap of score registers r, r + 1 (keys k, k + 1 in lane
         // half 0, k + 4, k + 5 in half 1, k = 8(r/4) + r%4) leaves queries
@@ -568,7 +574,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
     // O = acc / l for this lane's row.
     auto epilogue = [&]() __attribute__((always_inline)) {
       const float lt = sum_with_other_half(l_run);
-      if constexpr (kD16) {
+      if constexpr (kNarrowD) {
         // Block 0: query base + l % 16, block 1: base + 16 + l % 16; d = 4(l/16) + e.
         float lt_lo, lt_hi;
         by_query16(lt, lt_lo, lt_hi);
@@ -754,7 +760,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
         const float a = fast_exp2(m_run - mu);
         const float bb = fast_exp2(ml[0] - mu);
         l_run = __builtin_fmaf(l_run, a, ml[1] * bb);
-        if constexpr (kD16) {
+        if constexpr (kNarrowD) {
           // Factors per output block (queries l % 16 and 16 + l % 16).
           float a_lo, a_hi, b_lo, b_hi;
           by_query16(a, a_lo, a_hi);
