@@ -479,6 +479,35 @@ def test_folded_grid_one_round(gpu_ready, batch, seq_len, heads, head_dim, mask_
         assert bool((actual[1, :200] == 0).all())
 
 
+@pytest.mark.parametrize("case_seed", range(24))
+def test_randomized_grid_filling_shapes(gpu_ready, case_seed):
+    # Random shapes large enough for the fp32 schedules that only appear on
+    # full grids: the paired grid (ceil(nq/2)*B*H >= 2 workgroups per CU),
+    # the folded one-round grid (CUs < nq*B*H <= 2*CUs) and the plain
+    # heaviest-first grid, with causal or not, key masks with left padding
+    # and holes, head dims 8-64 and BSHD or packed layouts.  Two heads (the
+    # first and a random one) of every batch element go to the oracle.
+    rng = torch.Generator().manual_seed(7000 + case_seed)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731
+    batch = int(torch.randint(2, 9, (1,), generator=rng))
+    heads = int(torch.randint(12, 41, (1,), generator=rng))
+    seq_len = int(torch.randint(300, 1301, (1,), generator=rng))
+    head_dim = pick([8, 16, 32, 64])
+    causal = bool(torch.randint(4, (1,), generator=rng)) != 0  # mostly causal
+    layout = pick(["contiguous", "packed"])
+    q, k, v = _layout_inputs((batch, seq_len, heads, head_dim), layout, rng)
+    pad = torch.randint(0, seq_len // 3, (batch, 1), generator=rng)
+    mask = (torch.arange(seq_len)[None, :] >= pad) & (torch.rand(batch, seq_len, generator=rng) > 0.15)
+    actual = run_hip(q, k, v, mask, causal)
+    other = int(torch.randint(1, heads, (1,), generator=rng))
+    for hh in (0, other):
+        sl = slice(hh, hh + 1)
+        reference = oracle(q[:, :, sl].cpu(), k[:, :, sl].cpu(), v[:, :, sl].cpu(), mask, causal)
+        assert contract_failures(actual[:, :, sl], reference) == 0, (
+            f"B={batch} S={seq_len} H={heads} D={head_dim} causal={causal} layout={layout} head={hh}")
+        tight_check(actual[:, :, sl], reference, torch.float32)
+
+
 def _layout_inputs(shape, layout: str, rng: torch.Generator, dtype=torch.float32):
     """q, k, v on the GPU as contiguous BSHD, permuted BHSD views or packed-QKV views."""
     batch, seq_len, heads, head_dim = shape
