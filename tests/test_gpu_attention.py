@@ -7,7 +7,7 @@ oracle and the kernel see identical bytes.  Two bounds are asserted:
     - fp32 and fp16: the reference's ``|d| <= 1e-3 or |d| <= 0.01*|ref|``
       (tests/test_gpu_attention.py:53-62);
     - bf16 (no reference route exists, config.py:17-18; bound stated here):
-      ``|d| <= 1e-2 or |d| <= 0.02*|ref|`` and mean |d| <= 1e-3.  P is rounded
+      ``|d| <= 1e-2 or |d| <= 0.02*|ref|`` and mean |d| <= 1e-3 + 2e-3*mean|ref|.  P is rounded
       to bf16 (8 significant bits) for the P.V MFMA, so one output element can
       move by up to ~2^-9 * max|v| (~6e-3 at 3-sigma v) even when |out| is
       small; the output rounding adds 2^-9 relative.
@@ -92,14 +92,21 @@ CONTRACT = {
 }
 
 
-def contract_failures(actual: torch.Tensor, reference: torch.Tensor, bf16_mean: float = 1e-3) -> int:
-    """Elements outside the dtype's contract (finite and |d|<=atol or <=rtol*|ref|)."""
+def contract_failures(actual: torch.Tensor, reference: torch.Tensor, bf16_mean: float | None = None) -> int:
+    """Elements outside the dtype's contract (finite and |d|<=atol or <=rtol*|ref|).
+
+    bf16 also bounds the mean error, by default 1e-3 + 2e-3 * mean|ref|: rounding
+    the output to bf16 alone averages 2^-10 to 2^-9 of |ref|, which reaches 1e-3
+    when short rows leave outputs of magnitude ~1 (a long row averages them down).
+    """
     atol, rtol = CONTRACT[actual.dtype]
     a = actual.float().cpu()
     r = reference.float().cpu()
     err = (a - r).abs()
     ok = torch.isfinite(a) & ((err <= atol) | (err <= rtol * r.abs()))
     if actual.dtype == torch.bfloat16 and err.numel():
+        if bf16_mean is None:
+            bf16_mean = 1e-3 + 2e-3 * r.abs().mean().item()
         assert err.mean().item() <= bf16_mean, f"bf16 mean abs error {err.mean().item():.3g}"
     return int((~ok).sum().item())
 
@@ -350,8 +357,7 @@ def test_negative_zero_and_large_scales(gpu_ready, dtype, head_dim, causal, mask
         # bf16 rounds P and the output to 8 significant bits, so the mean
         # error grows with |out|: at scale 0.9 the softmax is peaked and the
         # outputs are about |v|, not an average over many keys.
-        bf16_mean = 1e-3 + 2e-3 * reference.abs().mean().item()
-        assert contract_failures(actual, reference, bf16_mean) == 0, f"scale={scale}"
+        assert contract_failures(actual, reference) == 0, f"scale={scale}"
         if scale == 0.0:
             keys = torch.ones(shape[0], shape[1], dtype=torch.bool) if mask is None else mask
             allowed = keys[:, None, :].expand(shape[0], shape[1], shape[1])  # [b, query, key]
