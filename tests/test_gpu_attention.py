@@ -535,6 +535,7 @@ def _layout_inputs(shape, layout: str, rng: torch.Generator, dtype=torch.float32
     (4, 64, 2, 8, "none", "packed"),
     (1, 64, 7, 64, "prefix", "bhsd"),
     (2, 32, 3, 64, "holes", "contiguous"),
+    (2, 50, 3, 128, "holes", "bhsd"),      # head_dim 128: 64-key tiles when non-causal
 ])
 def test_twin_grid_short_sequences(gpu_ready, batch, seq_len, heads, head_dim, mask_mode, layout):
     # fp32 non-causal attention with S <= 64 (one key tile; a 128-query tile
