@@ -249,8 +249,9 @@ constexpr int kMinWaves = (D >= 128 && F32) ? 1 : 2;
 template <int D, bool CAUSAL>
 struct F32Cfg {
   // Keys per tile.  Head dim 128 runs one workgroup per CU; 64-key tiles fit
-  // its LDS and halve the barriers (non-causal +5-7 %), but with the causal
-  // hand-off state they spill 14-49 registers, so causal keeps 32-key tiles.
+  // its LDS and halve the barriers (non-causal +5-7 %), but the causal
+  // variants then spill 14-51 registers (with or without the diagonal
+  // hand-off), so causal keeps 32-key tiles.
   static constexpr int BN = (D >= 128 && CAUSAL) ? 32 : 64;
   static constexpr int NSB = BN / 32;               // 32-key sub-blocks per tile
   static constexpr int CPR = D / 4;                 // 16-byte chunks per key row
