@@ -17,7 +17,11 @@ Also reported in the same line:
   summary in profiles/traffic.json when present, else null;
 * ``cpu_baseline``: the reference's explicit PyTorch attention (the oracle's
   restatement, kind "port") timed on this host's cores on a bounded sample of
-  the same workload;
+  the same workload (``value``), plus the explicit residual+LayerNorm (GB/s)
+  and the explicit encoder (tokens/s, configs 1 and 4) beside it;
+* ``clock_settle``: untimed launches of the step for ``--settle-s`` seconds
+  before the W warm-up steps, so the K timed steps do not include the GPU's
+  clock ramp;
 * ``secondary``: the S sweep {256..4096} causal/non-causal (config 2), the
   residual+LayerNorm HBM GB/s per hidden size with rotating input sets larger
   than the 256 MB MALL (config 3), bf16 long-sequence attention (config 5a)
@@ -107,6 +111,31 @@ def attention_tflops(batch, seq_len, heads, head_dim, causal, dtype, steps=10, w
     return attention_flops(batch, heads, seq_len, head_dim, causal) / (med * 1e-3) / 1e12, med
 
 
+def packed_attention_5b_us(steps: int = 50, warmup: int = 5) -> float:
+    """Average launch (us) of the config-5b encoder's attention: fp32, non-causal,
+    [512, 64, 8, 64] on the unbind views of one packed [512, 64, 3, 8, 64]
+    projection, between two events around ``steps`` back-to-back launches."""
+    import torch
+
+    from transformer_opt.kernels import hip_attention
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    packed = torch.randn(512, 64, 3, 8, 64, device="cuda", generator=g)
+    q, k, v = packed.unbind(dim=2)
+    out = torch.empty(512, 64, 8, 64, device="cuda")
+    for _ in range(warmup):
+        hip_attention(q, k, v, causal=False, out=out)
+    torch.cuda.synchronize()
+    begin = torch.cuda.Event(enable_timing=True)
+    finish = torch.cuda.Event(enable_timing=True)
+    begin.record()
+    for _ in range(steps):
+        hip_attention(q, k, v, causal=False, out=out)
+    finish.record()
+    torch.cuda.synchronize()
+    return begin.elapsed_time(finish) / steps * 1e3
+
+
 def layer_norm_gbps(hidden: int, rows: int = 32768, steps: int = 50, warmup: int = 5):
     """Config 3: rotate input sets so their total exceeds the 256 MB MALL.
 
@@ -180,16 +209,58 @@ def model_tokens_per_second(dtype_name: str, cfg=ENCODER_CONFIG4, steps: int = 5
     return batch * seq_len * 1000.0 / med, med, replays
 
 
-def cpu_baseline(time_budget_s: float = 20.0):
-    """The reference's explicit attention on host cores, bounded sample.
+def _median_call_seconds(fn, min_calls: int, max_calls: int, budget_s: float) -> tuple:
+    """One untimed warm-up call, then perf_counter_ns per call (the reference's
+    timer, benchmarks/torch_transformer_benchmark.py:501-506) until at least
+    ``min_calls`` calls and the budget or ``max_calls`` is reached."""
+    fn()
+    samples = []
+    t_start = time.perf_counter()
+    while len(samples) < min_calls or (time.perf_counter() - t_start < budget_s
+                                       and len(samples) < max_calls):
+        t0 = time.perf_counter_ns()
+        fn()
+        samples.append((time.perf_counter_ns() - t0) / 1e9)
+    return statistics.median(samples), len(samples)
 
-    Times the oracle restatement of the explicit PyTorch attention
-    (reference transformer_opt/dispatch.py:69-96) on the config-2 workload
-    (fp32, causal, S=1024, D=64), one batch element (16 heads) per call, for
-    as many calls as fit the budget (at least 5 after one warm-up), and
-    reports algorithmic causal TFLOP/s.
+
+def _cpu_model_tokens_per_second(cfg, batch: int, min_calls: int, budget_s: float) -> dict:
+    """The organizer's explicit encoder (oracle restatement of benchmarks/
+    torch_transformer_benchmark.py:59-172) on ``batch`` sequences of ``cfg``."""
+    import torch
+
+    from oracle.model import BaselineTransformer, TransformerConfig
+
+    config = TransformerConfig(batch, *cfg[1:])
+    torch.manual_seed(1234)
+    model = BaselineTransformer(config).eval()
+    x = torch.randn(batch, config.seq_len, config.d_model, generator=torch.Generator().manual_seed(3))
+    with torch.inference_mode():
+        med, calls = _median_call_seconds(lambda: model(x), min_calls, 20, budget_s)
+    return {"tokens_per_s": round(batch * config.seq_len / med, 1), "ms": round(med * 1e3, 2),
+            "calls": calls}
+
+
+def cpu_baseline(time_budget_s: float = 8.0):
+    """The reference's explicit PyTorch path on host cores, bounded samples.
+
+    All three CPU paths the baseline plan names, timed in this process on
+    identically generated fp32 inputs, median per call after a warm-up:
+
+    * attention (``value``): the oracle restatement of the explicit attention
+      (reference transformer_opt/dispatch.py:69-96) on the config-2 workload
+      (causal, S=1024, D=64), one of the 8 batch elements (16 heads) per call,
+      as algorithmic causal TFLOP/s;
+    * residual + LayerNorm: ``x + u`` then ``F.layer_norm`` (the reference's
+      explicit order) on config 3 rows=32768, hidden=1024, as GB/s of the same
+      algorithmic bytes the GPU figure uses;
+    * the explicit encoder (benchmarks/torch_transformer_benchmark.py:59-172):
+      config 1 (B=2, S=128, d=256, 1 layer, the reference's CPU-runnable
+      case) and one of the 4 sequences of config 4 (S=2048, d=1024, 6 layers,
+      causal), as tokens/s.
     """
     import torch
+    import torch.nn.functional as F
 
     sys.path.insert(0, str(REPO))
     from oracle.attention import kernel_contract_attention
@@ -199,15 +270,24 @@ def cpu_baseline(time_budget_s: float = 20.0):
     g = torch.Generator().manual_seed(7)
     shape = (1, 1024, 16, 64)
     q, k, v = (torch.randn(shape, generator=g) for _ in range(3))
-    kernel_contract_attention(q, k, v, None, True)  # warm-up
-    samples = []
-    t_start = time.perf_counter()
-    while len(samples) < 5 or (time.perf_counter() - t_start < time_budget_s and len(samples) < 50):
-        t0 = time.perf_counter_ns()
-        kernel_contract_attention(q, k, v, None, True)
-        samples.append((time.perf_counter_ns() - t0) / 1e9)
-    med = statistics.median(samples)
-    tflops = attention_flops(1, 16, 1024, 64, True) / med / 1e12
+    att_s, att_calls = _median_call_seconds(
+        lambda: kernel_contract_attention(q, k, v, None, True), 5, 50, time_budget_s)
+    tflops = attention_flops(1, 16, 1024, 64, True) / att_s / 1e12
+
+    rows, hidden = 32768, 1024
+    x = torch.randn(rows, hidden, generator=g)
+    u = torch.randn(rows, hidden, generator=g)
+    w = torch.rand(hidden, generator=g) + 0.5
+    b = torch.randn(hidden, generator=g) * 0.1
+
+    def residual_norm():
+        r = x + u
+        return r, F.layer_norm(r, (hidden,), w, b, 1e-5)
+
+    ln_s, ln_calls = _median_call_seconds(residual_norm, 5, 50, time_budget_s / 2)
+    del x, u
+    model_1 = _cpu_model_tokens_per_second((2, 128, 256, 4, 1024, 1, False), 2, 5, 2.0)
+    model_4 = _cpu_model_tokens_per_second(ENCODER_CONFIG4, 1, 3, 1.0)
     return {
         "value": tflops,
         "unit": "TFLOP/s",
@@ -215,8 +295,15 @@ def cpu_baseline(time_budget_s: float = 20.0):
         "kind": "port",
         "sample": (f"explicit PyTorch attention (oracle restatement of reference dispatch.py:69-96), "
                    f"fp32 causal, 1 of 8 batch elements of [8,1024,16,64] per call, median of "
-                   f"{len(samples)} calls ({med * 1e3:.1f} ms each); os.cpu_count()={os.cpu_count()}, "
+                   f"{att_calls} calls ({att_s * 1e3:.1f} ms each); os.cpu_count()={os.cpu_count()}, "
                    f"cpu={platform.processor() or platform.machine()}"),
+        "residual_layernorm": {
+            "gbps": round(layer_norm_bytes(rows, hidden) / ln_s / 1e9, 2), "ms": round(ln_s * 1e3, 2),
+            "calls": ln_calls,
+            "sample": "x + u then F.layer_norm, fp32 [32768, 1024] (config 3 at hidden 1024)"},
+        "model_config1": dict(model_1, sample="explicit encoder, fp32, B=2 S=128 d=256 H=4 FFN 1024, 1 layer"),
+        "model_config4": dict(model_4, sample="explicit encoder, fp32, 1 of 4 sequences of config 4 "
+                                              "(S=2048 d=1024 H=16 FFN 4096, 6 layers, causal)"),
     }
 
 
@@ -372,6 +459,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=50)
     parser.add_argument("--quick", action="store_true", help="skip the secondary measurements")
+    parser.add_argument("--settle-s", type=float, default=1.0,
+                        help="seconds of untimed launches before the warm-up (clock settling)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "layernorm_bf16", "copy", "attention_bf16",
                                                    "attention_bf16_d64", "attention_5b", "encoder_fp32", "encoder_bf16",
@@ -412,6 +501,18 @@ def main() -> int:
     def step():
         hip_attention(q, k, v, causal=True, out=out)
 
+    # Clock settling: the GPU leaves its idle clock only after some
+    # sustained work, so the headline would otherwise time the ramp when the
+    # warm-up is short.  Launch the step for a fixed wall time before the W
+    # warm-up steps; the JSON line reports it.
+    settle_launches = 0
+    settle_t0 = time.perf_counter()
+    while time.perf_counter() - settle_t0 < args.settle_s:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+        settle_launches += 20
+    settle_s = time.perf_counter() - settle_t0
     for _ in range(args.warmup):
         step()
     # The kernel is launched on torch's current stream, so events recorded on
@@ -460,6 +561,8 @@ def main() -> int:
             "kernel": "attn_fwd_f32_kernel<64, causal>",
             "launch_us": round(avg_launch_ms * 1e3, 2),
         },
+        "clock_settle": {"launches": settle_launches, "seconds": round(settle_s, 3),
+                         "note": "untimed launches of the step before the warm-up"},
     }
     del q, k, v, out
     torch.cuda.empty_cache()
@@ -486,6 +589,20 @@ def main() -> int:
             "tflops": round(tf, 2), "ms": round(ms, 3),
             "frac_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
         log(f"attention bf16 causal long-sequence: {tf:.1f} TF")
+        torch.cuda.empty_cache()
+        # The attention of the config-4 bf16 encoder and of the config-5b
+        # encoder (non-causal fp32 on packed-QKV views), per launch.
+        tf, ms = attention_tflops(4, 2048, 16, 64, True, torch.bfloat16, steps=20, warmup=5)
+        secondary["attention_bf16_causal_B4_H16_S2048_D64"] = {
+            "tflops": round(tf, 2), "us": round(ms * 1e3, 2),
+            "frac_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
+        log(f"attention bf16 causal [4,2048,16,64]: {tf:.1f} TF ({ms * 1e3:.1f} us)")
+        us = packed_attention_5b_us()
+        tf = attention_flops(512, 8, 64, 64, False) / (us * 1e-6) / 1e12
+        secondary["attention_fp32_noncausal_B512_H8_S64_D64_packed"] = {
+            "tflops": round(tf, 2), "us": round(us, 2),
+            "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+        log(f"attention fp32 config-5b layer: {tf:.1f} TF ({us:.1f} us)")
         torch.cuda.empty_cache()
         ln = {}
         for hidden in (256, 512, 768, 1024, 4096):
@@ -524,7 +641,7 @@ def main() -> int:
         result["secondary"] = secondary
 
     if not args.no_cpu_baseline:
-        log("timing the CPU baseline (explicit PyTorch attention)")
+        log("timing the CPU baseline (explicit PyTorch attention, residual+LN, encoder)")
         result["cpu_baseline"] = cpu_baseline()
         result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 5)
     result["device"] = dev_name

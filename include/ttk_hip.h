@@ -59,6 +59,9 @@ const char* ttk_last_error(void);
  * key_valid: NULL, or a [B, S] byte mask (nonzero = valid) with element
  *   strides mask_strides[2] (mask_strides may be NULL when key_valid is).
  * D must be one of 8, 16, 32, 64, 128.
+ * Limits (TTK_EUNSUPPORTED beyond them): S <= 2^24; B * H * ceil(S / 128)
+ * <= 16777215 (2^32 - 1 work-items of 256-thread workgroups, the HIP grid
+ * limit); K and V sequence strides below 2^25 elements.
  *
  * Replaces the launch of `_attention_fwd` inside `triton_attention`
  * (reference transformer_opt/kernels/attention.py:268-360, kernel :103-265);
@@ -89,6 +92,11 @@ ttk_status ttk_attention_fwd(const void* q, const void* k, const void* v,
  * x, u, residual_out, normalized_out: rows*N contiguous elements of `dtype`;
  * w: N elements; b: N elements or NULL; row_valid: `rows` bytes or NULL
  * (required when either zeroing flag is set).
+ * Limits (TTK_EUNSUPPORTED beyond them): N <= 65536; the launch grid at most
+ * 16777215 workgroups - rows <= 16777215 for widths that take the
+ * one-workgroup-per-row path (N not a multiple of 16 bytes, unaligned
+ * buffers, or more than 16 vectors per lane), and 4 * 64 / lanes_per_row
+ * times that for the others (at least 4 * 16777215 rows).
  *
  * Replaces the launch of `_residual_layer_norm_fwd` inside
  * `fused_residual_layer_norm` (reference
@@ -132,7 +140,9 @@ ttk_status ttk_linear_gelu_fwd(const void* x, const void* w, const void* bias,
  * Exact (erf) GELU, elementwise: y[i] = x[i] * Phi(x[i]) for i < n, computed
  * in fp32 and rounded once to `dtype` (TTK_F32, TTK_BF16 or TTK_F16).  x and
  * y are contiguous; y == x (in place) is allowed, any other overlap is
- * TTK_EINVAL.  16-byte aligned buffers take the vector path.  n <= 2^38.
+ * TTK_EINVAL.  16-byte aligned buffers take the vector path.  n <=
+ * 4294967040 (2^32 - 256: an unaligned buffer runs one element per
+ * work-item), else TTK_EUNSUPPORTED.
  *
  * Replaces the separate GELU pass of the encoder's FFN,
  * `F.gelu(layer.ffn_in(ffn_input), approximate="none")` (reference

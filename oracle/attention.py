@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import math
 from typing import Optional
 
 import numpy as np
@@ -148,3 +149,133 @@ def brute_force_attention_f64(q, k, v, valid_token_mask=None, causal=False, scal
                 out[b, s, h] = sum(w * v[b, t, h] for w, t in zip(weights, keys))
     return out
 
+
+
+LOG2E_F32 = np.float32(1.4426950408889634)
+
+
+def _exp2_scale(head_dim: int, scale: Optional[float]) -> tuple:
+    """(sign, c): the kernel works on sign * scores with c = |fl32(scale * log2 e)|.
+
+    A negative scale is an exact sign flip of Q; scale 0 uses c = 2^-100 so
+    masked scores stay -inf and every allowed score gives the same P.
+    """
+    sc = np.float32(head_dim ** -0.5 if scale is None else scale)
+    c = float(np.float32(sc * LOG2E_F32))
+    sign = -1.0 if c < 0 else 1.0
+    c = abs(c)
+    return sign, (c if c != 0.0 else 2.0 ** -100)
+
+
+def kernel_rounding_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    valid_token_mask: Optional[torch.Tensor] = None,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    *,
+    heads: Optional[list] = None,
+    query_rows: Optional[slice] = None,
+) -> torch.Tensor:
+    """Attention with the 16-bit kernel's dtype boundaries, in float64.
+
+    The reference's low-precision explicit attention rounds the softmax
+    probabilities to the input dtype before P.V (transformer_opt/
+    dispatch.py:94); a flash kernel rounds the unnormalised probabilities
+    instead and divides by an fp32 row sum at the end.  This restates that
+    order so a bf16/fp16 kernel can be held to a tight bound:
+
+    * scores ``s = fl32(q . k)`` (exact products, one rounding to fp32), in
+      units of ``c = |fl32(scale * log2 e)|``;
+    * reference exponent ``M = ceil(fl32(max_allowed(s) * c))``, an integer;
+    * ``p = fl32(exp2(fl32(s * c - M)))``, then ``P = p`` rounded to the
+      input dtype (nearest even);
+    * output ``sum(P v) / sum(p)``; rows without an allowed key are zero.
+
+    Any integer in place of ``M`` gives the same result up to a power of two
+    that cancels in the division, so a kernel may move its reference lazily
+    as long as it stays an integer.  Inputs are ``[B, S, H, D]`` fp16/bf16
+    tensors; the result is float64 ``[B, S, H, D]``, or
+    ``[len(heads), rows, D]`` when ``heads`` selects (b, h) pairs.
+    """
+    batch, seq_len, num_heads, head_dim = q.shape
+    sign, c = _exp2_scale(head_dim, scale)
+    pairs = heads if heads is not None else [(b, h) for b in range(batch) for h in range(num_heads)]
+    rows = query_rows if query_rows is not None else slice(0, seq_len)
+    qpos = torch.arange(seq_len)[rows]
+    results = []
+    for b, h in pairs:
+        qh = q[b, rows, h, :].double() * sign
+        kh = k[b, :, h, :].double()
+        vh = v[b, :, h, :].double()
+        s = torch.matmul(qh, kh.transpose(0, 1)).float().double()
+        allowed = torch.ones((qh.shape[0], seq_len), dtype=torch.bool)
+        if causal:
+            allowed &= torch.arange(seq_len)[None, :] <= qpos[:, None]
+        if valid_token_mask is not None:
+            allowed &= valid_token_mask[b][None, :].to(torch.bool).cpu()
+        s = s.masked_fill(~allowed, float("-inf"))
+        any_allowed = allowed.any(dim=1)
+        m = s.max(dim=1).values.masked_fill(~any_allowed, 0.0)
+        ref = torch.ceil((m * c).float().double())
+        p = torch.exp2((s * c - ref[:, None]).float().double()).float()
+        rounded = p.to(q.dtype).double()
+        total = p.double().sum(dim=1, keepdim=True)
+        out = torch.matmul(rounded, vh) / total.clamp_min(torch.finfo(torch.float64).tiny)
+        results.append(out.masked_fill(~any_allowed[:, None], 0.0))
+    stacked = torch.stack(results)
+    if heads is not None:
+        return stacked
+    return stacked.view(batch, num_heads, -1, head_dim).transpose(1, 2).contiguous()
+
+
+def _round_bits_f32_to_bf16(x: np.float32) -> float:
+    """Nearest-even bf16 of a float32, by its bit pattern."""
+    bits = int(np.array(x, dtype=np.float32).view(np.uint32))
+    bits = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) << 16
+    return float(np.array(bits & 0xFFFFFFFF, dtype=np.uint32).view(np.float32))
+
+
+def brute_force_kernel_rounding_f64(q, k, v, valid_token_mask=None, causal=False, scale=None,
+                                    p_dtype: str = "bfloat16") -> np.ndarray:
+    """Independent loop statement of :func:`kernel_rounding_attention`.
+
+    Written from the definition, one query row at a time with numpy scalars:
+    logits rounded to float32 from float64 dot products, an integer reference
+    exponent ``ceil(float32(max * c))``, ``p = float32(2 ** float32(x * c -
+    M))``, P rounded to bf16 by its bit pattern (nearest even) or to fp16 by
+    numpy, output ``sum(P v) / sum(p)``.  ``p_dtype`` is "bfloat16",
+    "float16" or "float32" (no rounding of P).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    batch, seq_len, num_heads, head_dim = q.shape
+    sc = np.float32(head_dim ** -0.5 if scale is None else scale)
+    c = float(np.float32(sc * np.float32(1.4426950408889634)))
+    sign = -1.0 if c < 0 else 1.0
+    c = abs(c) if c != 0.0 else 2.0 ** -100
+    mask = None if valid_token_mask is None else np.asarray(valid_token_mask, dtype=bool)
+    rounders = {
+        "bfloat16": _round_bits_f32_to_bf16,
+        "float16": lambda x: float(np.float16(x)),
+        "float32": float,
+    }
+    round_p = rounders[p_dtype]
+    out = np.zeros_like(q)
+    for b in range(batch):
+        for h in range(num_heads):
+            for s in range(seq_len):
+                keys = [t for t in range(seq_len)
+                        if (not causal or t <= s) and (mask is None or mask[b, t])]
+                if not keys:
+                    continue
+                logits = [float(np.float32(sign * float(np.dot(q[b, s, h], k[b, t, h]))))
+                          for t in keys]
+                top = math.ceil(float(np.float32(max(logits) * c)))
+                p = [np.float32(2.0 ** float(np.float32(x * c - top))) for x in logits]
+                weights = [round_p(pi) for pi in p]
+                total = sum(float(pi) for pi in p)
+                out[b, s, h] = sum(w * v[b, t, h] for w, t in zip(weights, keys)) / total
+    return out

@@ -86,6 +86,29 @@ def test_layernorm_argument_errors_are_reported_without_launching():
     assert f(16, 16, 16, None, None, 16, 16, 0, 0, 128, 1e-5, 0, 0, None) == _native.TTK_OK
 
 
+def test_launch_grid_limits_are_unsupported_not_launch_failures():
+    # HIP refuses grids above 2^32 - 1 work-items (16777215 workgroups of 256):
+    # sizes the kernels cannot launch come back as TTK_EUNSUPPORTED before any
+    # HIP call, not as a failed launch.
+    lib = _native.load()
+    limit = 16777215
+    # attention: one workgroup per (batch, head, 128-query tile)
+    assert _attention(lib, B=limit + 1, H=1, S=16) == _native.TTK_EUNSUPPORTED
+    assert "launch limit" in _native.last_error()
+    assert _attention(lib, B=1 << 17, H=128, S=16) == _native.TTK_EUNSUPPORTED  # 2^24 groups
+    assert _attention(lib, B=1 << 10, H=1 << 7, S=129 * 128) == _native.TTK_EUNSUPPORTED
+    assert _attention(lib, B=1 << 40, H=1 << 40, S=16) == _native.TTK_EUNSUPPORTED  # no overflow
+    f = lib.ttk_residual_layernorm_fwd
+    # (x, u, w, b, valid, r_out, y_out, dtype, rows, N, eps, zr, zn, stream)
+    # width 7 (fp32) takes the one-workgroup-per-row path
+    assert f(16, 16, 16, None, None, 16, 16, 0, limit + 1, 7, 1e-5, 0, 0, None) == _native.TTK_EUNSUPPORTED
+    assert "launch limit" in _native.last_error()
+    # width 128 fp32: eight rows per wavefront, 32 rows per workgroup
+    assert f(16, 16, 16, None, None, 16, 16, 0, 32 * limit + 1, 128, 1e-5, 0, 0, None) == \
+        _native.TTK_EUNSUPPORTED
+    assert f(16, 16, 16, None, None, 16, 16, 0, 1 << 62, 128, 1e-5, 0, 0, None) == _native.TTK_EUNSUPPORTED
+
+
 def test_last_error_is_thread_local():
     lib = _native.load()
     assert _attention(lib, D=48) == _native.TTK_EUNSUPPORTED
@@ -152,7 +175,9 @@ def test_gelu_argument_errors_are_reported_without_launching():
     assert f(16, 16, 7, 8, None) == _native.TTK_EUNSUPPORTED
     assert "dtype" in _native.last_error()
     assert f(16, 16, _native.TTK_BF16, -1, None) == _native.TTK_EINVAL
-    assert f(16, 16, _native.TTK_BF16, (1 << 38) + 1, None) == _native.TTK_EINVAL
+    # One element per work-item on an unaligned buffer: n stops at 2^32 - 256.
+    assert f(16, 16, _native.TTK_BF16, 4294967040 + 1, None) == _native.TTK_EUNSUPPORTED
+    assert "launch limit" in _native.last_error()
     assert f(None, 16, _native.TTK_BF16, 8, None) == _native.TTK_EINVAL
     # y one element past x: overlapping but not in place.
     assert f(1024, 1026, _native.TTK_BF16, 8, None) == _native.TTK_EINVAL

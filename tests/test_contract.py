@@ -28,8 +28,10 @@ def _cpu_qkv(dtype=torch.float32):
     return q, torch.randn_like(q), torch.randn_like(q)
 
 
-def test_backends_are_auto_and_hip_only():
-    assert ATTENTION_BACKENDS == ("auto", "hip")
+def test_backends_name_only_the_hip_route():
+    # "triton" is the reference's forced fused route (config.py:11,
+    # dispatch.py:119-132); here it names the HIP kernel that replaces it.
+    assert ATTENTION_BACKENDS == ("auto", "hip", "triton")
     assert triton_attention_support is hip_attention_support
 
 
@@ -46,6 +48,13 @@ def test_cpu_tensors_fail_loudly_instead_of_falling_back():
     for backend in ("auto", "hip"):
         with pytest.raises((RuntimeError, ValueError), match="HIP attention was"):
             attention_forward(q, k, v, backend=backend)
+
+
+def test_forced_triton_route_fails_like_the_reference_on_cpu():
+    # Reference tests/test_dispatch.py:27-29 matches this wording.
+    q, k, v = _cpu_qkv()
+    with pytest.raises((RuntimeError, ValueError), match="Triton attention was forced"):
+        attention_forward(q, k, v, backend="triton")
 
 
 @pytest.mark.parametrize("bad,reason", [
@@ -104,7 +113,9 @@ def test_model_constructor_validation_and_state_surface():
     with pytest.raises(ValueError, match="execution_mode"):
         UserOptimizedTransformer(cfg, execution_mode="invalid")
     with pytest.raises(ValueError, match="attention_backend"):
-        UserOptimizedTransformer(cfg, attention_backend="triton")
+        UserOptimizedTransformer(cfg, attention_backend="sdpa")
+    forced = UserOptimizedTransformer(cfg, attention_backend="triton").eval()
+    assert forced._replay_refusal(torch.randn(1, 128, 128), None) == "attention backend is forced"
     model = UserOptimizedTransformer(cfg).eval()
     assert model.attention_backend_counts == {"hip": 0}
     assert model.fused_residual_layer_norm_calls == 0 and model.cuda_graph_replays == 0

@@ -6,13 +6,14 @@ oracle and the kernel see identical bytes.  Two bounds are asserted:
 * the contract, finite on every element and
     - fp32 and fp16: the reference's ``|d| <= 1e-3 or |d| <= 0.01*|ref|``
       (tests/test_gpu_attention.py:53-62);
-    - bf16 (no reference route exists, config.py:17-18; bound stated here):
-      ``|d| <= 1e-2 or |d| <= 0.02*|ref|`` and mean |d| <= 1e-3 + 2e-3*mean|ref|.  P is rounded
-      to bf16 (8 significant bits) for the P.V MFMA, so one output element can
-      move by up to ~2^-9 * max|v| (~6e-3 at 3-sigma v) even when |out| is
-      small; the output rounding adds 2^-9 relative.
-  The low-precision outputs are compared with the fp32 oracle evaluated on
-  the same rounded inputs.
+    - bf16 (no reference route exists, config.py:17-18; bound stated before
+      measuring): ``|d| <= 2e-3 or |d| <= 0.02*|ref|``, no mean-error term.
+  fp32 outputs are compared with the reference's explicit attention in fp32.
+  bf16/fp16 outputs are compared with the same attention evaluated at the
+  16-bit kernel's dtype boundaries (fp32 scores, probabilities rounded to the
+  input dtype before P.V against an integer reference exponent, fp32 row
+  sum; ``oracle.attention.kernel_rounding_attention``), on the same rounded
+  inputs.
 * a tighter accuracy bound for fp32 that catches systematic mistakes the
   loose contract can hide: ``|d| <= 2e-5 + 2e-5*|ref|`` at the default scale.
 """
@@ -26,6 +27,7 @@ from oracle.attention import (
     brute_force_attention_f64,
     chunked_kernel_contract_attention,
     kernel_contract_attention,
+    kernel_rounding_attention,
 )
 
 pytestmark = pytest.mark.gpu
@@ -85,29 +87,24 @@ def make_mask(mode: str, batch: int, seq_len: int):
     return torch.arange(seq_len)[None, :] < lengths[:, None]
 
 
+# |d| <= atol or |d| <= rtol * |ref| on every element, against the oracle of
+# the dtype (see ``oracle``): fp32 and fp16 the reference's contract
+# (torch_transformer_benchmark.py:309-319), bf16 the bound stated before
+# measuring for a dtype the reference has no fused route for.
 CONTRACT = {
     torch.float32: (1e-3, 1e-2),
     torch.float16: (1e-3, 1e-2),
-    torch.bfloat16: (1e-2, 2e-2),
+    torch.bfloat16: (2e-3, 2e-2),
 }
 
 
-def contract_failures(actual: torch.Tensor, reference: torch.Tensor, bf16_mean: float | None = None) -> int:
-    """Elements outside the dtype's contract (finite and |d|<=atol or <=rtol*|ref|).
-
-    bf16 also bounds the mean error, by default 1e-3 + 2e-3 * mean|ref|: rounding
-    the output to bf16 alone averages 2^-10 to 2^-9 of |ref|, which reaches 1e-3
-    when short rows leave outputs of magnitude ~1 (a long row averages them down).
-    """
+def contract_failures(actual: torch.Tensor, reference: torch.Tensor) -> int:
+    """Elements outside the dtype's contract (finite and |d|<=atol or <=rtol*|ref|)."""
     atol, rtol = CONTRACT[actual.dtype]
     a = actual.float().cpu()
     r = reference.float().cpu()
     err = (a - r).abs()
     ok = torch.isfinite(a) & ((err <= atol) | (err <= rtol * r.abs()))
-    if actual.dtype == torch.bfloat16 and err.numel():
-        if bf16_mean is None:
-            bf16_mean = 1e-3 + 2e-3 * r.abs().mean().item()
-        assert err.mean().item() <= bf16_mean, f"bf16 mean abs error {err.mean().item():.3g}"
     return int((~ok).sum().item())
 
 
@@ -139,8 +136,38 @@ def run_hip(q, k, v, mask, causal, scale=None):
     return out.cpu()
 
 
+def test_forced_triton_backend_runs_the_hip_kernel(gpu_ready):
+    # Reference callers force backend="triton" (tests/test_gpu_attention.py:
+    # 99-180, tests/test_dispatch.py:29); here that route is the HIP kernel.
+    from transformer_opt import attention_forward
+
+    g = torch.Generator().manual_seed(5)
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        q, k, v = (torch.randn(2, 77, 3, 64, generator=g).to(dtype).cuda() for _ in range(3))
+        mask = make_mask("prefix", 2, 77)
+        with torch.inference_mode():
+            out, decision = attention_forward(q, k, v, mask.cuda(), causal=True, backend="triton")
+            hip, _ = attention_forward(q, k, v, mask.cuda(), causal=True, backend="hip")
+        assert (decision.requested, decision.selected) == ("triton", "hip")
+        assert torch.equal(out, hip)
+        assert contract_failures(out.cpu(), oracle(q.cpu(), k.cpu(), v.cpu(), mask, True)) == 0
+    with torch.inference_mode(), pytest.raises(ValueError, match="Triton attention was forced"):
+        bad = torch.randn(1, 8, 2, 48, device="cuda")
+        attention_forward(bad, bad, bad, backend="triton")
+
+
 def oracle(q, k, v, mask, causal, scale=None):
-    """fp32 explicit attention on the (already rounded) inputs."""
+    """The checker of each dtype, on the (already rounded) inputs.
+
+    fp32: the reference's explicit attention in fp32 with the kernel's
+    all-masked-row contract.  bf16/fp16: the same attention with the 16-bit
+    kernel's dtype boundaries - fp32 scores, probabilities rounded to the
+    input dtype before P.V against an integer reference exponent, fp32 row
+    sum (oracle.attention.kernel_rounding_attention) - so the bound measures
+    the kernel, not the rounding of P that any 16-bit P.V performs.
+    """
+    if q.dtype in (torch.bfloat16, torch.float16):
+        return kernel_rounding_attention(q, k, v, mask, causal, scale).float()
     return kernel_contract_attention(q.float(), k.float(), v.float(), mask, causal, scale)
 
 
@@ -400,6 +427,26 @@ def test_permuted_layouts_and_strided_mask(gpu_ready, dtype, causal):
     tight_check(actual, reference, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_contiguous_views_at_unaligned_offsets(gpu_ready, dtype):
+    # buf[1:].view(B, S, H, D) is contiguous but starts one element past a
+    # 16-byte boundary; the wrapper copies it to aligned storage instead of
+    # refusing an input the reference accepts.
+    from transformer_opt.kernels import hip_attention
+
+    g = torch.Generator().manual_seed(61)
+    B, S, H, D = 2, 70, 2, 64
+    n = B * S * H * D
+    bufs = [torch.randn(n + 1, generator=g).to(dtype).cuda() for _ in range(3)]
+    q, k, v = (b[1:].view(B, S, H, D) for b in bufs)
+    assert all(t.is_contiguous() and t.data_ptr() % 16 != 0 for t in (q, k, v))
+    with torch.inference_mode():
+        out = hip_attention(q, k, v, causal=True)
+        aligned = hip_attention(q.clone(), k.clone(), v.clone(), causal=True)
+    assert torch.equal(out, aligned)
+    assert contract_failures(out.cpu(), oracle(q.cpu(), k.cpu(), v.cpu(), None, True)) == 0
+
+
 def test_empty_batch_returns_empty(gpu_ready):
     for dtype in (torch.float32, torch.bfloat16):
         q = torch.empty(0, 16, 2, 64, dtype=dtype)
@@ -632,20 +679,19 @@ def test_randomized_shapes_layouts_and_masks(gpu_ready, case_seed):
 
 
 @pytest.mark.parametrize("seq_len", [1024, 4096])
-def test_baseline_size_rows_match_chunked_oracle(gpu_ready, seq_len):
-    # BASELINE config 2 geometry (B=8, H=16, D=64, fp32); the oracle checks a
-    # sample of heads, the kernel runs the full batch.
+def test_baseline_size_every_head_matches_chunked_oracle(gpu_ready, seq_len):
+    # BASELINE config 2 geometry (B=8, H=16, D=64, fp32), causal and not:
+    # the chunked oracle evaluates all 128 (batch, head) pairs, so every
+    # output element of the full-size launch is compared.
     g = torch.Generator().manual_seed(29)
     shape = (8, seq_len, 16, 64)
     q, k, v = (torch.randn(shape, generator=g) for _ in range(3))
     for causal in (True, False):
         out = run_hip(q, k, v, None, causal)
-        heads = [(0, 0), (3, 7), (7, 15)]
-        reference = chunked_kernel_contract_attention(q, k, v, None, causal, heads=heads)
-        actual = torch.stack([out[b, :, h, :] for b, h in heads])
-        assert contract_failures(actual, reference) == 0
+        reference = chunked_kernel_contract_attention(q, k, v, None, causal)
+        actual = out.permute(0, 2, 1, 3).reshape(8 * 16, seq_len, 64)
+        assert contract_failures(actual, reference) == 0, f"causal={causal}"
         tight_check(actual, reference, torch.float32)
-        assert torch.isfinite(out).all()
 
 
 def test_determinism_bitwise(gpu_ready):
@@ -659,9 +705,9 @@ def test_determinism_bitwise(gpu_ready):
 
 def test_config5a_long_sequence_bf16_rows_and_memory(gpu_ready):
     # BASELINE config 5a: causal bf16, B=1, H=32, S=16384, D=128, run at full
-    # size.  Query rows are independent, so the chunked oracle on sampled
-    # (head, row-block) pairs - start, middle and end of the sequence, where
-    # the rows meet 128 to 16384 keys - checks those rows of the full run.
+    # size.  Query rows are independent, so the chunked oracle on every head
+    # at four row blocks - start, middle and end of the sequence, where the
+    # rows meet 128 to 16384 keys - checks those rows of the full run.
     # Memory: the kernel keeps no workspace, so with a caller-owned output a
     # launch allocates nothing at all.
     from transformer_opt.kernels import hip_attention
@@ -682,9 +728,8 @@ def test_config5a_long_sequence_bf16_rows_and_memory(gpu_ready):
     assert torch.cuda.max_memory_allocated() == before
     result = out.cpu()
     assert torch.isfinite(result).all()
-    pairs = [(0, 0), (0, 17), (0, 31)]
-    qf, kf, vf = q.float(), k.float(), v.float()
-    for rows in (slice(0, 128), slice(8128, 8256), slice(16256, 16384)):
-        reference = chunked_kernel_contract_attention(qf, kf, vf, None, True, heads=pairs, query_rows=rows)
+    pairs = [(0, h) for h in range(heads)]
+    for rows in (slice(0, 128), slice(5000, 5128), slice(8128, 8256), slice(16256, 16384)):
+        reference = kernel_rounding_attention(q, k, v, None, True, heads=pairs, query_rows=rows)
         actual = torch.stack([result[b, rows, h, :] for b, h in pairs])
         assert contract_failures(actual, reference) == 0, f"rows {rows}"

@@ -208,9 +208,9 @@ def test_packed_qkv_cache_is_reused_and_invalidated(gpu_ready):
     x = torch.randn(1, 32, 64)
     with torch.inference_mode():
         first = model(x.cuda())
-        first_packed = model._packed_qkv_cache[id(model.layers[0].attention)][1]
+        first_packed = model._packed_qkv_cache[0].weight
         second = model(x.cuda())
-    assert model._packed_qkv_cache[id(model.layers[0].attention)][1] is first_packed
+    assert model._packed_qkv_cache[0].weight is first_packed
     assert torch.equal(first, second)
     with torch.no_grad():
         baseline.layers[0].attention.q_proj.weight.add_(0.01)
@@ -218,7 +218,7 @@ def test_packed_qkv_cache_is_reused_and_invalidated(gpu_ready):
     with torch.inference_mode():
         ref = baseline(x)
         out = model(x.cuda())
-    assert model._packed_qkv_cache[id(model.layers[0].attention)][1] is not first_packed
+    assert model._packed_qkv_cache[0].weight is not first_packed
     assert compare_outputs(ref, out, rtol=0.01, atol=0.001).passed
 
 
@@ -235,46 +235,48 @@ def _bf16_rounded_oracle(baseline):
     return baseline
 
 
+def _assert_low_precision_model(got, ref):
+    # bf16/fp16 encoders against the fp32 oracle on the same rounded weights
+    # and input: |d| <= 5e-2 or |d| <= 0.05*|ref| on every element, mean |d|
+    # <= 1e-2 (the low-precision model gate stated before measuring).
+    err = (got - ref).abs()
+    ok = (err <= 5e-2) | (err <= 0.05 * ref.abs())
+    assert bool(ok.all()), f"failed={int((~ok).sum())} max_abs={err.max().item():.3g}"
+    assert err.mean().item() <= 1e-2
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
-def test_config4_full_size_matches_oracle_on_causal_prefix(gpu_ready, dtype):
+def test_config4_full_size_matches_oracle_on_every_element(gpu_ready, dtype):
     # BASELINE config 4 at full size on the GPU (6 layers, d=1024, H=16,
-    # FFN 4096, B=4, S=2048, causal), through the hipGraph replay path.  With
-    # causal attention and every other op row-wise, output positions < P
-    # depend only on input positions < P, so the CPU oracle run on the first
-    # P positions checks those rows of the full-size forward exactly.
+    # FFN 4096, B=4, S=2048, causal), through the hipGraph replay path, and
+    # the CPU oracle over the same full input: every one of the 4 x 2048 x
+    # 1024 outputs is compared.
     cfg = TransformerConfig(4, 2048, 1024, 16, 4096, 6, True)
     baseline, model = build(cfg, dtype=dtype, seed=41)
     x = torch.randn(4, 2048, 1024, generator=torch.Generator().manual_seed(42)).to(dtype)
     if dtype == torch.bfloat16:
         baseline = _bf16_rounded_oracle(baseline)
-    prefix = 256
     with torch.inference_mode():
         out = model(x.cuda())
-        ref = baseline(x[:, :prefix].float())
+        got = out.float().cpu()
+        ref = baseline(x.float())
     assert model.cuda_graph_replays == 1
     assert out.dtype == dtype and out.shape == (4, 2048, 1024)
-    assert bool(torch.isfinite(out).all())
-    head = out[:, :prefix].float().cpu()
+    assert bool(torch.isfinite(got).all())
     if dtype == torch.float32:
-        res = compare_outputs(ref, head, rtol=0.01, atol=0.001)
+        res = compare_outputs(ref, got, rtol=0.01, atol=0.001)
         assert res.passed, f"failed={res.failed_elements} max_abs={res.max_abs_error:.3e} at {res.worst_index}"
     else:
-        err = (head - ref).abs()
-        ok = (err <= 5e-2) | (err <= 0.05 * ref.abs())
-        assert bool(ok.all()), f"failed={int((~ok).sum())} max_abs={err.max().item():.3g}"
-        assert err.mean().item() <= 1e-2
+        _assert_low_precision_model(got, ref)
 
 
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
 def test_config4_full_size_fp16_key_padding(gpu_ready, causal):
     # fp16 with a key-padding mask at the config-4 model size (6 layers,
-    # d=1024, H=16, FFN 4096, B=4, S=2048), through the hipGraph replay path.
-    # Sequence lengths 2048, 1531, 200 and 37 put masked keys inside every
-    # checked region: causal - the oracle on the first P positions (outputs
-    # there see only keys < P); non-causal - the oracle on whole sequences of
-    # two batch elements (batch elements never interact).  Bound as for the
-    # smaller fp16 model; rows the mask invalidates are exact zeros over the
-    # whole output.
+    # d=1024, H=16, FFN 4096, B=4, S=2048), through the hipGraph replay path,
+    # against the oracle on the whole batch.  Sequence lengths 2048, 1531,
+    # 200 and 37 put masked keys into every sequence but the first; rows the
+    # mask invalidates are exact zeros.
     cfg = TransformerConfig(4, 2048, 1024, 16, 4096, 6, causal)
     baseline, model = build(cfg, dtype=torch.float16, seed=45)
     baseline.load_state_dict({k: v.to(torch.float16).float() for k, v in baseline.state_dict().items()})
@@ -284,39 +286,28 @@ def test_config4_full_size_fp16_key_padding(gpu_ready, causal):
     x = x.masked_fill(~mask[..., None], 0).to(torch.float16)
     with torch.inference_mode():
         out = model(x.cuda(), mask.cuda())
-        if causal:
-            prefix = 256
-            ref = baseline(x[:, :prefix].float(), mask[:, :prefix])
-            got = out[:, :prefix].float().cpu()
-        else:
-            picks = torch.tensor([1, 3])
-            ref = baseline(x[picks].float(), mask[picks])
-            got = out[picks.cuda()].float().cpu()
+        got = out.float().cpu()
+        ref = baseline(x.float(), mask)
     assert model.cuda_graph_replays == 1
     assert out.dtype == torch.float16 and out.shape == (4, 2048, 1024)
-    full = out.float().cpu()
-    assert bool(torch.isfinite(full).all())
-    assert bool((full[~mask] == 0).all())
-    err = (got - ref).abs()
-    ok = (err <= 5e-2) | (err <= 0.05 * ref.abs())
-    assert bool(ok.all()), f"failed={int((~ok).sum())} max_abs={err.max().item():.3g}"
-    assert err.mean().item() <= 1e-2
+    assert bool(torch.isfinite(got).all())
+    assert bool((got[~mask] == 0).all())
+    _assert_low_precision_model(got, ref)
 
 
-def test_config5b_huge_batch_encoder_matches_oracle_on_batch_subset(gpu_ready):
+def test_config5b_huge_batch_encoder_matches_oracle_on_every_element(gpu_ready):
     # BASELINE config 5b at full size: B=512, S=64, d=512, H=8 (D=64), 4
     # layers, fp32, hipGraph replay.  The FFN width is not stated there; 4*d
-    # (2048) as in configs 1 and 4, and an encoder (non-causal) stack.  Batch
-    # elements never interact, so the oracle on a subset of them checks those
-    # rows of the full-batch forward exactly.
+    # (2048) as in configs 1 and 4, and an encoder (non-causal) stack.  The
+    # oracle runs the same 512 sequences; every output is compared.
     cfg = TransformerConfig(512, 64, 512, 8, 2048, 4, False)
     baseline, model = build(cfg, seed=43)
     x = torch.randn(512, 64, 512, generator=torch.Generator().manual_seed(44))
-    picks = torch.tensor([0, 1, 137, 300, 511])
     with torch.inference_mode():
         out = model(x.cuda())
-        ref = baseline(x[picks])
+        got = out.cpu()
+        ref = baseline(x)
     assert model.cuda_graph_replays == 1
-    assert bool(torch.isfinite(out).all())
-    res = compare_outputs(ref, out[picks.cuda()].cpu(), rtol=0.01, atol=0.001)
+    assert bool(torch.isfinite(got).all())
+    res = compare_outputs(ref, got, rtol=0.01, atol=0.001)
     assert res.passed, f"failed={res.failed_elements} max_abs={res.max_abs_error:.3e} at {res.worst_index}"

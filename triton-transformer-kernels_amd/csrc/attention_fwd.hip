@@ -1059,18 +1059,23 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       }
     };
 
-    // Lazy reference max: probabilities are exp2((s - m_run) * c) against a
-    // per-row reference m_run that moves only when the row's max exceeds it
-    // by more than 8 / c (so P <= 2^8); the accumulator and the row sum are
-    // rescaled only then, for the whole wavefront at once.  Call after the
-    // P.V MFMAs that use the previous reference have been issued.
+    // Lazy reference max: probabilities are exp2(s * c - ceil(m_run * c))
+    // against a per-row reference m_run that moves only when the row's max
+    // exceeds it by more than 8 / c (so P <= 2^8); the accumulator and the
+    // row sum are rescaled only then, for the whole wavefront at once.  The
+    // reference exponent is rounded up to an integer, so P = 2^k * exp2(s * c
+    // - ceil(max * c)) for an integer k whatever the lag: rounding P to 16
+    // bits lands on the same grid as rounding it against the final row max
+    // (a power-of-two scale commutes with rounding), and the rescale factor
+    // is an exact power of two.  Call after the P.V MFMAs that use the
+    // previous reference have been issued.
     auto rebase = [&](float mt) __attribute__((always_inline)) {
       const bool need = (mt - m_run) * c > 8.0f;  // false for two -inf
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
         const float m_new = need ? mt : m_run;
         // 1 where the reference stays (also at -inf, where the difference
-        // would be NaN), 0 from -inf, else < 1.
-        const float alpha = m_new == m_run ? 1.0f : fast_exp2((m_run - m_new) * c);
+        // would be NaN), 0 from -inf, else 2^-k.
+        const float alpha = m_new == m_run ? 1.0f : fast_exp2(ceilf(m_run * c) - ceilf(m_new * c));
         l_run *= alpha;
 #pragma unroll
         for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
@@ -1086,7 +1091,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
       mt = max_with_other_half(mt);
       rebase(mt);
-      const float mc = ((MASKED && m_run == -INFINITY) ? 0.0f : m_run) * c;
+      const float mc = ceilf(((MASKED && m_run == -INFINITY) ? 0.0f : m_run) * c);
       float ls = 0.0f;
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
@@ -1133,8 +1138,8 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
             // 1 where the reference stays: a row still at -inf (no allowed
             // key so far) must not turn its zeros into NaN when another row
             // of the wavefront moves.
-            alpha = m_use == m_run ? 1.0f : fast_exp2((m_run - m_use) * c);
-            mc = ((MASKED && m_use == -INFINITY) ? 0.0f : m_use) * c;
+            alpha = m_use == m_run ? 1.0f : fast_exp2(ceilf(m_run * c) - ceilf(m_use * c));
+            mc = ceilf(((MASKED && m_use == -INFINITY) ? 0.0f : m_use) * c);
           }
         } else {
 #pragma unroll

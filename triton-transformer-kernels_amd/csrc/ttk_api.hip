@@ -38,6 +38,9 @@ int elem_bytes(int dtype) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 constexpr int64_t kIntMax = std::numeric_limits<int>::max();
+// HIP launches at most 2^32 - 1 work-items per grid dimension; every kernel
+// here runs 256-thread workgroups on a 1-D grid.
+constexpr int64_t kMaxGroups = int64_t{0xFFFFFFFF} / 256;
 
 }  // namespace
 
@@ -79,7 +82,14 @@ extern "C" ttk_status ttk_attention_fwd(const void* q, const void* k, const void
   }
   const int64_t bm = ttk::attention_block_m(dtype, static_cast<int>(D));
   const int64_t nq = (S + bm - 1) / bm;
-  if (B * H > kIntMax / nq) return fail(TTK_EUNSUPPORTED, "attention: grid too large");
+  // The largest grid any schedule launches is one workgroup per (batch,
+  // head, 128-query tile).
+  if (B > kMaxGroups || H > kMaxGroups || B * H > kMaxGroups / nq) {
+    return fail(TTK_EUNSUPPORTED,
+                "attention: B*H*ceil(S/%lld) workgroups exceed the launch limit %lld "
+                "(B=%lld S=%lld H=%lld)",
+                (long long)bm, (long long)kMaxGroups, (long long)B, (long long)S, (long long)H);
+  }
   const void* ptrs[4] = {q, k, v, out};
   const int64_t* strides[4] = {q_strides, k_strides, v_strides, o_strides};
   const char* names[4] = {"q", "k", "v", "out"};
@@ -156,7 +166,6 @@ extern "C" ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u, c
   if (!x || !w || !normalized_out) {
     return fail(TTK_EINVAL, "layernorm: x, weight and normalized_out must not be NULL");
   }
-  if (rows > kIntMax) return fail(TTK_EUNSUPPORTED, "layernorm: too many rows (%lld)", (long long)rows);
 
   ttk::LnParams p{};
   p.x = x;
@@ -197,6 +206,17 @@ extern "C" ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u, c
       p.lanes_per_row = lpr;
       vpl = static_cast<int>(per_lane);
     }
+  }
+  // Grid of the chosen path: one workgroup per row (fallback) or per four
+  // wavefronts of 64 / lanes_per_row rows each (vector path).
+  const int64_t groups = vector_path
+      ? ((rows + 64 / p.lanes_per_row - 1) / (64 / p.lanes_per_row) + 3) / 4
+      : rows;
+  if (groups > kMaxGroups) {
+    return fail(TTK_EUNSUPPORTED,
+                "layernorm: %lld rows of width %lld need %lld workgroups, above the launch "
+                "limit %lld",
+                (long long)rows, (long long)N, (long long)groups, (long long)kMaxGroups);
   }
   const hipError_t err = ttk::launch_residual_layernorm(dtype, p, vector_path, vpl,
                                                         static_cast<hipStream_t>(stream));
@@ -260,8 +280,11 @@ extern "C" ttk_status ttk_gelu_fwd(const void* x, void* y, int dtype, int64_t n,
   g_error[0] = '\0';
   const int es = elem_bytes(dtype);
   if (es == 0) return fail(TTK_EUNSUPPORTED, "gelu: unsupported dtype code %d", dtype);
-  if (n < 0 || n > (int64_t{1} << 38)) {
-    return fail(TTK_EINVAL, "gelu: element count %lld outside [0, 2^38]", (long long)n);
+  if (n < 0) return fail(TTK_EINVAL, "gelu: negative element count %lld", (long long)n);
+  // An unaligned buffer runs one element per work-item.
+  if (n > kMaxGroups * 256) {
+    return fail(TTK_EUNSUPPORTED, "gelu: element count %lld exceeds the launch limit %lld",
+                (long long)n, (long long)(kMaxGroups * 256));
   }
   if (n == 0) return TTK_OK;
   if (!x || !y) return fail(TTK_EINVAL, "gelu: x and y must not be NULL");

@@ -5,8 +5,11 @@ Mirrors the reference's ``transformer_opt/config.py``: the same Q/K/V contract
 that explains every refusal (reference ``triton_attention_support``,
 config.py:143-175).  What changes is the envelope of the hardware path:
 
-* backends are ``auto`` and ``hip`` only - there is no SDPA or explicit-math
-  fallback in the product path;
+* backends are ``auto``, ``hip`` and ``triton``, and all three run the HIP
+  kernel: ``triton`` is the reference's name for its forced fused route
+  (config.py:11, dispatch.py:119-132), kept so callers that force it land on
+  the kernel that replaces it.  There is no SDPA or explicit-math route in
+  the product path;
 * dtypes are fp32, bf16 and fp16 (the reference stopped at fp16/fp32,
   config.py:17-18);
 * sequence length is bounded by the kernel's index range, not by a measured
@@ -22,7 +25,9 @@ from typing import Optional
 
 import torch
 
-ATTENTION_BACKENDS = ("auto", "hip")
+ATTENTION_BACKENDS = ("auto", "hip", "triton")
+# Backends a caller may force; each names the HIP kernel.
+FORCED_BACKENDS = frozenset({"hip", "triton"})
 SUPPORTED_HEAD_DIMS = frozenset({8, 16, 32, 64, 128})
 SUPPORTED_DTYPES = frozenset({torch.float32, torch.bfloat16, torch.float16})
 MAX_SEQUENCE_LENGTH = 1 << 24

@@ -55,13 +55,15 @@ def hip_attention(
         raise ValueError(f"unsupported HIP attention input: {support.reason}")
 
     # Arbitrary B/S/H strides are part of the contract; rows that are not
-    # 16-byte aligned are repacked so the kernel keeps its vector loads.
+    # 16-byte aligned are copied into fresh (aligned) storage so the kernel
+    # keeps its vector loads - also for a contiguous view at an odd storage
+    # offset, which ``contiguous()`` would return unchanged.
     if not _vector_ready(q):
-        q = q.contiguous()
+        q = q.clone(memory_format=torch.contiguous_format)
     if not _vector_ready(k):
-        k = k.contiguous()
+        k = k.clone(memory_format=torch.contiguous_format)
     if not _vector_ready(v):
-        v = v.contiguous()
+        v = v.clone(memory_format=torch.contiguous_format)
 
     batch, seq_len, num_heads, head_dim = q.shape
     if out is None:

@@ -7,36 +7,43 @@
 ``cuda_graph_replays``, ``reset_attention_backend_counts()``,
 ``clear_cuda_graph()``, ``_can_replay_cuda_graph()``, a state-dict key set
 identical to the organizer baseline, a non-persistent packed-QKV projection
-cache invalidated by parameter versions, and bounded graph replay.
+and hipGraph replay.
 
-What is MI355X-specific:
+How a forward runs here:
 
-* every attention runs on the HIP kernel (fp32, bf16, fp16) - the
-  reference's per-shape routing policy between Triton, SDPA and explicit math
-  (submission.py:235-321) is gone, and so is the SDPA counter;
-* every LayerNorm runs on the HIP fused residual + LayerNorm kernel, in the
-  reference's fused order (submission.py:481-525) for all shapes: one
-  standalone norm, then two fused residual+norm calls per layer;
-* the packed QKV projection is used for every width and dtype
-  (submission.py:184-190 restricted it to measured widths);
-* graph replay (torch.cuda.CUDAGraph, i.e. a hipGraph on ROCm) is eligible for
-  every supported shape and dtype instead of an exact measured shape set
-  (submission.py:582-590), and up to ``max_cuda_graphs`` captures (one per
-  input geometry: shape, dtype, mask presence, inference mode) are kept, so a
-  caller alternating between shapes replays instead of recapturing.
+1. ``_operands()`` reads, once, every tensor and scalar the forward uses -
+   LayerNorm weights and eps, the packed QKV projection, attention heads and
+   scale, the output and FFN projections - into a flat ``_Operands`` record,
+   and fingerprints that read set (tensor identity, storage and version;
+   the scalars; module training flags and hooks).  The fingerprint is the
+   capture key: a capture is stale exactly when something it read changed.
+2. ``_encode(ops, x, mask, tally)`` is the forward over those operands: one
+   standalone LayerNorm, then per block attention, a fused residual +
+   LayerNorm, the FFN, and a fused residual + LayerNorm that also produces
+   the next block's (or the final) normalised input - the fused order of the
+   reference (submission.py:481-525).  Every kernel launch is reported to
+   ``tally``.
+3. ``forward`` either runs ``_encode`` eagerly or replays a hipGraph of it
+   from ``replay.ReplayCache``; ``_replay_refusal`` names the rule that keeps
+   a call eager.
 
-Projections and the FFN stay library GEMMs (hipBLASLt through F.linear); the
-FFN's exact GELU runs in place on the HIP elementwise kernel (the fused
-Linear + GELU kernel, kernels.linear_gelu, measured no faster in the model).
-The model is forward-inference only: a call with gradients enabled on
-parameters that require them raises, as there is no backward kernel.
+What is MI355X-specific: every attention runs on the HIP kernel (fp32,
+bf16, fp16) and every LayerNorm on the HIP residual + LayerNorm kernel - the
+reference's per-shape routing between Triton, SDPA and explicit math
+(submission.py:235-321) is gone, and so is the SDPA counter; the packed QKV
+projection is used for every width and dtype (submission.py:184-190
+restricted it); graph replay is eligible for every supported shape and dtype
+instead of a measured shape set (submission.py:582-590), with up to
+``max_cuda_graphs`` captures kept, one per input geometry.  Projections and
+the FFN are library GEMMs (hipBLASLt through ``F.linear``); the FFN's exact
+GELU runs in place on the HIP elementwise kernel.  The model is
+forward-inference only: with gradients enabled on parameters that require
+them the kernels raise, as there is no backward kernel.
 """
 
 from __future__ import annotations
 
-import threading
-from collections import OrderedDict
-from typing import Dict, Optional, Tuple
+from typing import Dict, NamedTuple, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -46,11 +53,142 @@ from .config import ATTENTION_BACKENDS, SUPPORTED_DTYPES
 from .dispatch import attention_forward
 from .kernels.gelu import gelu_
 from .kernels.residual_layer_norm import fused_residual_layer_norm, layer_norm
-from .model import SelfAttention, TransformerBlock, TransformerConfig
+from .model import TransformerBlock, TransformerConfig
+from .replay import CallTally, CapturedForward, ReplayCache, tensor_stamp
 
 __all__ = ["TransformerConfig", "UserOptimizedTransformer", "generate_random_case", "run_accuracy_tests"]
 
 _EXECUTION_MODES = ("auto", "eager")
+
+
+class _Norm(NamedTuple):
+    weight: torch.Tensor
+    bias: Optional[torch.Tensor]
+    eps: float
+
+
+class _Block(NamedTuple):
+    """Operands of one encoder block, read from its modules."""
+
+    qkv_weight: torch.Tensor  # [3 * d_model, d_model]
+    qkv_bias: torch.Tensor
+    num_heads: int
+    head_dim: int
+    scale: float
+    out_weight: torch.Tensor
+    out_bias: Optional[torch.Tensor]
+    norm2: _Norm
+    ffn_in_weight: torch.Tensor
+    ffn_in_bias: Optional[torch.Tensor]
+    ffn_out_weight: torch.Tensor
+    ffn_out_bias: Optional[torch.Tensor]
+    exit_norm: _Norm  # the next block's norm1, or the final norm
+
+
+class _Operands(NamedTuple):
+    entry_norm: _Norm  # the first block's norm1
+    blocks: Tuple[_Block, ...]
+    # Hashable summary of everything above (None: the read set cannot be
+    # fingerprinted - inference-tensor parameters, training mode or hooks).
+    fingerprint: Optional[tuple]
+    keepalive: tuple  # tensors a capture reads by address
+
+
+class _Layout:
+    """Where the forward's operands sit in the module tree, read once.
+
+    ``slots`` holds one ``(dict, key, object)`` triple per edge the forward
+    walks - child modules and parameters - so ``intact()`` is a single
+    identity pass.  ``tensors`` are the parameters whose stamps key a
+    capture; ``modules`` those whose training flag and hooks do.
+    """
+
+    __slots__ = ("epoch", "slots", "modules", "tensors", "norms", "attentions", "layers",
+                 "final_norm")
+
+    def __init__(self, model: "UserOptimizedTransformer", epoch: int) -> None:
+        self.epoch = epoch
+        slots, modules, tensors = [], [model], []
+
+        def child(parent: nn.Module, name: str) -> nn.Module:
+            module = parent._modules[name]
+            slots.append((parent._modules, name, module))
+            modules.append(module)
+            return module
+
+        def param(owner: nn.Module, name: str) -> Optional[torch.Tensor]:
+            tensor = owner._parameters.get(name)
+            slots.append((owner._parameters, name, tensor))
+            if tensor is not None:
+                tensors.append(tensor)
+            return tensor
+
+        stack = child(model, "layers")
+        self.layers = []
+        self.norms = []
+        self.attentions = []
+        for name in list(stack._modules):
+            layer = child(stack, name)
+            norm1, attn = child(layer, "norm1"), child(layer, "attention")
+            projections = [child(attn, p) for p in ("q_proj", "k_proj", "v_proj", "out_proj")]
+            norm2, ffn_in, ffn_out = (child(layer, n) for n in ("norm2", "ffn_in", "ffn_out"))
+            entry = {
+                "norm1": (param(norm1, "weight"), param(norm1, "bias")),
+                "qkv": tuple(param(p, "weight") for p in projections[:3])
+                + tuple(param(p, "bias") for p in projections[:3]),
+                "out": (param(projections[3], "weight"), param(projections[3], "bias")),
+                "norm2": (param(norm2, "weight"), param(norm2, "bias")),
+                "ffn_in": (param(ffn_in, "weight"), param(ffn_in, "bias")),
+                "ffn_out": (param(ffn_out, "weight"), param(ffn_out, "bias")),
+            }
+            self.layers.append(entry)
+            self.norms += [norm1, norm2]
+            self.attentions.append(attn)
+        final = child(model, "final_norm")
+        self.final_norm = (param(final, "weight"), param(final, "bias"))
+        self.norms.append(final)
+        self.slots = tuple(slots)
+        self.modules = tuple(modules)
+        self.tensors = tuple(tensors)
+
+    def intact(self) -> bool:
+        return all(d.get(k) is v for d, k, v in self.slots)
+
+    def scalars(self) -> tuple:
+        return (tuple([n.eps for n in self.norms]),
+                tuple([(a.num_heads, a.head_dim, a.d_model, a.scale) for a in self.attentions]))
+
+    def resolve(self, cache: ReplayCache) -> _Operands:
+        eps = [n.eps for n in self.norms]
+        exits = [_Norm(*entry["norm1"], eps[2 * i]) for i, entry in enumerate(self.layers)]
+        exits.append(_Norm(*self.final_norm, eps[-1]))
+        blocks = []
+        for index, (entry, attn) in enumerate(zip(self.layers, self.attentions)):
+            qkv = entry["qkv"]
+            pack = cache.pack_for(index, qkv[:3], qkv[3:])
+            blocks.append(_Block(
+                pack.weight, pack.bias, attn.num_heads, attn.head_dim, attn.scale,
+                *entry["out"], _Norm(*entry["norm2"], eps[2 * index + 1]),
+                *entry["ffn_in"], *entry["ffn_out"], exits[index + 1],
+            ))
+        keepalive = (self.tensors, tuple(cache.packs.values()))
+        return _Operands(exits[0], tuple(blocks), None, keepalive)
+
+
+class _ModelTally:
+    """Adapter that reports launches straight into the model's counters."""
+
+    __slots__ = ("model",)
+
+    def __init__(self, model: "UserOptimizedTransformer") -> None:
+        self.model = model
+
+    def count_attention(self, selected: str) -> None:
+        counts = self.model.attention_backend_counts
+        counts[selected] = counts.get(selected, 0) + 1
+
+    def count_fused_norm(self) -> None:
+        self.model.fused_residual_layer_norm_calls += 1
 
 
 class UserOptimizedTransformer(nn.Module):
@@ -75,309 +213,206 @@ class UserOptimizedTransformer(nn.Module):
         self.final_norm = nn.LayerNorm(config.d_model)
         self.attention_backend = attention_backend
         self.execution_mode = execution_mode
-        # Captured forwards keyed by input geometry, least recently used first;
-        # all of them belong to one model state (``_graph_model_key``).
-        self.max_cuda_graphs = max_cuda_graphs
-        self._inference_graphs: "OrderedDict[tuple, _InferenceGraph]" = OrderedDict()
-        self._graph_model_key = None
-        self._inference_graph = None  # the entry used last
-        self._inference_graph_lock = threading.RLock()
         self.cuda_graph_replays = 0
         self.attention_backend_counts: Dict[str, int] = {"hip": 0}
         self.fused_residual_layer_norm_calls = 0
-        # Derived, non-persistent packed projection weights keyed by module id;
-        # kept out of the state dict so its keys equal the baseline's.
-        self._packed_qkv_cache: Dict[int, Tuple[tuple, torch.Tensor, torch.Tensor]] = {}
+        # Captures, packed projections and the lock: derived inference state,
+        # outside the state dict and not copied with the module.
+        self._replay = ReplayCache(max_cuda_graphs)
 
-    # -- counters / pickling -------------------------------------------------
+    # -- surface ---------------------------------------------------------------
+    @property
+    def max_cuda_graphs(self) -> int:
+        return self._replay.capacity
+
+    @property
+    def _inference_graph(self) -> Optional[CapturedForward]:
+        """The capture the last replayed forward used (None after a drop)."""
+        return self._replay.last
+
+    @property
+    def _inference_graphs(self):
+        return self._replay.entries
+
+    @property
+    def _packed_qkv_cache(self) -> dict:
+        return dict(self._replay.packs)
+
     def reset_attention_backend_counts(self) -> None:
         self.attention_backend_counts = {"hip": 0}
         self.fused_residual_layer_norm_calls = 0
         self.cuda_graph_replays = 0
 
-    def __getstate__(self):
-        state = super().__getstate__().copy()
-        state["_inference_graph"] = None
-        state["_inference_graphs"] = OrderedDict()
-        state["_graph_model_key"] = None
-        state.pop("_inference_graph_lock", None)
-        return state
-
-    def __setstate__(self, state):
-        super().__setstate__(state)
-        self._inference_graph_lock = threading.RLock()
-
-    # -- projections -----------------------------------------------------------
-    @staticmethod
-    def _qkv_signature(attn: SelfAttention) -> tuple:
-        tensors = (attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight,
-                   attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias)
-        return tuple((t.data_ptr(), t._version, t.device, t.dtype) for t in tensors if t is not None)
-
-    def _project_qkv(self, attn: SelfAttention, x: torch.Tensor):
-        """One packed GEMM -> strided [B, S, H, D] views of Q, K and V.
-
-        Same cache contract as the reference (submission.py:145-217): the
-        concatenated weight is rebuilt whenever any projection parameter's
-        pointer, version counter, device or dtype changes.
-        """
-        batch, seq_len, _ = x.shape
-        signature = self._qkv_signature(attn)
-        cached = self._packed_qkv_cache.get(id(attn))
-        if cached is None or cached[0] != signature:
-            packed_weight = torch.cat(
-                (attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight), dim=0).detach()
-            packed_bias = torch.cat(
-                (attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias), dim=0).detach()
-            cached = (signature, packed_weight, packed_bias)
-            self._packed_qkv_cache[id(attn)] = cached
-        projected = F.linear(x, cached[1], cached[2])
-        qkv = projected.view(batch, seq_len, 3, attn.num_heads, attn.head_dim)
-        return qkv.unbind(dim=2)
-
-    def _attention(self, attn: SelfAttention, x: torch.Tensor,
-                   valid_token_mask: Optional[torch.Tensor], causal: bool) -> torch.Tensor:
-        batch, seq_len, _ = x.shape
-        q, k, v = self._project_qkv(attn, x)
-        context, dispatch = attention_forward(
-            q, k, v, valid_token_mask, causal=causal, scale=attn.scale,
-            backend=self.attention_backend,
-        )
-        self.attention_backend_counts[dispatch.selected] += 1
-        return attn.out_proj(context.reshape(batch, seq_len, attn.d_model))
-
-    def _fused_residual_norm(self, x, update, norm: nn.LayerNorm, valid_token_mask, *,
-                             zero_invalid_residual=False, zero_invalid_normalized=False):
-        residual, normalized = fused_residual_layer_norm(
-            x, update, norm.weight, norm.bias, norm.eps, valid_token_mask,
-            zero_invalid_residual=zero_invalid_residual,
-            zero_invalid_normalized=zero_invalid_normalized,
-        )
-        self.fused_residual_layer_norm_calls += 1
-        return residual, normalized
-
-    # -- forward -----------------------------------------------------------------
-    def _forward_eager(self, x: torch.Tensor,
-                       valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Fused order of the reference (submission.py:481-525).
-
-        LN(x) once; then per layer: attention, (x, ffn_in) = x + attn,
-        LN2(x + attn); FFN; (x, next_in) = x + ffn, next LN, with invalid rows
-        of x zeroed (the baseline's per-block masked_fill) and invalid rows of
-        the final output zeroed.  Invalid rows never reach a valid row: their
-        keys are masked in every attention and all other ops are row-wise.
-        """
-        if valid_token_mask is not None and not valid_token_mask.is_contiguous():
-            valid_token_mask = valid_token_mask.contiguous()
-        x = x.contiguous()
-        causal = self.config.causal
-        first = self.layers[0].norm1
-        normalized = layer_norm(x, first.weight, first.bias, first.eps)
-        last_index = len(self.layers) - 1
-        for index, layer in enumerate(self.layers):
-            attn_out = self._attention(layer.attention, normalized, valid_token_mask, causal)
-            del normalized
-            x, ffn_input = self._fused_residual_norm(x, attn_out, layer.norm2, valid_token_mask)
-            del attn_out
-            ffn_out = layer.ffn_out(gelu_(layer.ffn_in(ffn_input)))
-            del ffn_input
-            is_last = index == last_index
-            next_norm = self.final_norm if is_last else self.layers[index + 1].norm1
-            x, normalized = self._fused_residual_norm(
-                x, ffn_out, next_norm, valid_token_mask,
-                zero_invalid_residual=valid_token_mask is not None,
-                zero_invalid_normalized=is_last and valid_token_mask is not None,
-            )
-            del ffn_out
-        return normalized
-
-    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        if self._graph_input_supported(x, valid_token_mask):
-            with self._inference_graph_lock:
-                signature = self._graph_signature(x, valid_token_mask)
-                if signature is not None:
-                    model_key, geometry = signature
-                    if model_key != self._graph_model_key:
-                        # Parameters, modules or attention settings changed:
-                        # every capture is stale (and would pin old storage).
-                        self._drop_graphs()
-                        self._graph_model_key = model_key
-                    entry = self._inference_graphs.get(geometry)
-                    if entry is None:
-                        entry = _InferenceGraph(self, x, valid_token_mask, signature)
-                        self._inference_graphs[geometry] = entry
-                        while len(self._inference_graphs) > self.max_cuda_graphs:
-                            self._inference_graphs.popitem(last=False)
-                    else:
-                        self._inference_graphs.move_to_end(geometry)
-                    self._inference_graph = entry
-                    output = entry.replay(x, valid_token_mask)
-                    for backend, count in entry.backend_counts.items():
-                        self.attention_backend_counts[backend] += count
-                    self.fused_residual_layer_norm_calls += entry.fused_calls
-                    self.cuda_graph_replays += 1
-                    return output
-        return self._forward_eager(x, valid_token_mask)
-
-    # -- graph replay ------------------------------------------------------------
-    def _can_replay_cuda_graph(self, x, valid_token_mask) -> bool:
-        return (self._graph_input_supported(x, valid_token_mask)
-                and self._graph_signature(x, valid_token_mask) is not None)
-
-    def _graph_input_supported(self, x, valid_token_mask) -> bool:
-        """Capture eligibility (reference submission.py:561-601, minus the
-        measured-shape whitelist): eval-mode inference on one ROCm device with a
-        supported dtype, no autograd, no autocast, no hooks, not already
-        capturing."""
-        if (
-            self.execution_mode != "auto"
-            or self.attention_backend != "auto"
-            or not x.is_cuda
-            or x.dtype not in SUPPORTED_DTYPES
-            or x.ndim != 3
-            or not x.is_contiguous()
-            or torch.is_grad_enabled()
-            or self.training
-            or torch.compiler.is_compiling()
-            or torch.cuda.current_device() != x.device.index
-            or torch.cuda.is_current_stream_capturing()
-            or torch.is_autocast_enabled("cuda")
-        ):
-            return False
-        if x.shape[2] != self.config.d_model or x.numel() == 0:
-            return False
-        if x.dtype != self.final_norm.weight.dtype or x.device != self.final_norm.weight.device:
-            return False
-        if valid_token_mask is not None and not (
-            valid_token_mask.shape == x.shape[:2]
-            and valid_token_mask.device == x.device
-            and valid_token_mask.dtype == torch.bool
-            and valid_token_mask.is_contiguous()
-        ):
-            return False
-        if nn.modules.module._global_forward_hooks or nn.modules.module._global_forward_pre_hooks:
-            return False
-        return True
-
-    def _graph_signature(self, x, valid_token_mask):
-        """Everything a captured graph bakes in (reference submission.py:603-641),
-        as ``(model_key, geometry)``: the model key holds parameter
-        storage/version/device/dtype, module eps and shapes, hooks, training
-        flags and the attention config; the geometry holds the input's device,
-        shape and dtype, mask presence and the inference-mode context.  None
-        means "do not capture"."""
-        stack = [self]
-        seen_modules, seen_parameters = set(), set()
-        modules, parameters = [], []
-        while stack:
-            module = stack.pop()
-            identity = id(module)
-            if identity in seen_modules:
-                continue
-            seen_modules.add(identity)
-            if module.training or module._forward_hooks or module._forward_pre_hooks:
-                return None
-            modules.append((identity, getattr(module, "eps", None),
-                            getattr(module, "normalized_shape", None)))
-            for parameter in module._parameters.values():
-                if parameter is None or id(parameter) in seen_parameters:
-                    continue
-                seen_parameters.add(id(parameter))
-                if parameter.is_inference():
-                    return None
-                parameters.append((id(parameter), parameter.data_ptr(), parameter._version,
-                                   parameter.device, parameter.dtype))
-            stack.extend(child for child in reversed(tuple(module._modules.values()))
-                         if child is not None)
-        attention_config = tuple(
-            (layer.attention.d_model, layer.attention.num_heads,
-             layer.attention.head_dim, layer.attention.scale)
-            for layer in self.layers
-        )
-        model_key = (tuple(parameters), tuple(modules), attention_config, self.config,
-                     self.attention_backend, torch.backends.cuda.matmul.allow_tf32)
-        geometry = (x.device, tuple(x.shape), x.dtype, valid_token_mask is not None,
-                    torch.is_inference_mode_enabled())
-        return model_key, geometry
-
-    def _drop_graphs(self) -> None:
-        self._inference_graphs.clear()
-        self._inference_graph = None
-        self._graph_model_key = None
-
     def clear_cuda_graph(self) -> None:
         """Release every cached capture; a later eligible call rebuilds what it needs."""
-        with self._inference_graph_lock:
-            self._drop_graphs()
+        with self._replay.lock:
+            self._replay.drop_captures()
 
     def _apply(self, fn, recurse=True):
-        # Device/dtype moves must not keep the old graph pool or packed weights.
-        self.clear_cuda_graph()
-        self._packed_qkv_cache.clear()
+        # A device or dtype move replaces every parameter's storage: release
+        # captures (and their graph pools) and packed weights now rather than
+        # at the next forward.
+        self._replay.reset()
         return super()._apply(fn, recurse=recurse)
 
+    # -- operand resolution ----------------------------------------------------------
+    def _operands(self) -> _Operands:
+        """Operands for ``_encode`` and the fingerprint of everything they hold.
 
-class _InferenceGraph:
-    """One captured forward with static input buffers (reference submission.py:
-    674-723): warm up on a side stream, capture ``_forward_eager``, record the
-    backend counts the capture performed, and on replay copy fresh inputs in,
-    replay, and return a clone so earlier results are never overwritten."""
-
-    def __init__(self, model: UserOptimizedTransformer, x, mask, signature):
-        # Warm-up and capture run with inference mode off.  torch allocates the
-        # generator's graph-safe RNG state tensors at the first capture and
-        # updates them in place at every later one; allocated inside inference
-        # mode they would become inference tensors and a later capture outside
-        # it would fail.  Replay clones the output in the caller's context, so
-        # returned tensors still follow the caller's mode.
-        with torch.inference_mode(False), torch.no_grad():
-            self._capture(model, x, mask, signature)
-
-    def _capture(self, model: UserOptimizedTransformer, x, mask, signature):
-        self.signature = signature
-        self.x = x.clone()
-        self.mask = mask.clone() if mask is not None else None
-        # Keep captured parameter storage alive across state/device changes.
-        self.parameters = tuple(parameter.detach() for parameter in model.parameters())
-        before = dict(model.attention_backend_counts)
-        fused_before = model.fused_residual_layer_norm_calls
-        stream = torch.cuda.Stream(device=x.device)
-        current = torch.cuda.current_stream(x.device)
-        stream.wait_stream(current)
+        The tree layout (which module and parameter objects sit where) is
+        read once and re-checked per call with one identity pass; tensor
+        stamps (storage pointer, version) and the scalar settings (eps,
+        heads, scale) are re-read per call.  Operands are rebuilt only when
+        one of these moved.
+        """
+        cache = self._replay
+        layout = cache.layout
+        if layout is None or not layout.intact():
+            layout = _Layout(self, cache.layout_epoch + 1)
+            cache.layout, cache.layout_epoch, cache.operands = layout, layout.epoch, None
         try:
-            with torch.cuda.stream(stream):
-                for _ in range(3):
-                    model._forward_eager(self.x, self.mask)
-            current.wait_stream(stream)
-            capture_before = dict(model.attention_backend_counts)
-            capture_fused_before = model.fused_residual_layer_norm_calls
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph, stream=stream):
-                self.output = model._forward_eager(self.x, self.mask)
-            current.wait_stream(stream)
-            self.backend_counts = {
-                backend: count - capture_before.get(backend, 0)
-                for backend, count in model.attention_backend_counts.items()
-            }
-            self.fused_calls = model.fused_residual_layer_norm_calls - capture_fused_before
-            self.packed = tuple(model._packed_qkv_cache.values())
-            self.complete = torch.cuda.Event()
-            self.complete.record(current)
-        finally:
-            # Warm-up and capture are set-up, not user-visible forwards.
-            model.attention_backend_counts = before
-            model.fused_residual_layer_norm_calls = fused_before
+            stamps = tuple([(t.data_ptr(), t._version) for t in layout.tensors])
+        except RuntimeError:  # inference tensors carry no version counter
+            stamps = None
+        scalars = layout.scalars()
+        settled = not any(m.training or m._forward_hooks or m._forward_pre_hooks
+                          for m in layout.modules)
+        key = (layout.epoch, stamps, scalars)
+        ops = cache.operands
+        if ops is None or stamps is None or cache.operands_key != key:
+            ops = layout.resolve(cache)
+            cache.operands, cache.operands_key = ops, key
+        fingerprint = None
+        if stamps is not None and settled:
+            fingerprint = key + (self.config, torch.backends.cuda.matmul.allow_tf32)
+        return ops._replace(fingerprint=fingerprint)
 
-    def replay(self, x, mask):
-        current = torch.cuda.current_stream(x.device)
-        current.wait_event(self.complete)
-        self.x.copy_(x)
-        if self.mask is not None:
-            self.mask.copy_(mask)
-        self.graph.replay()
-        output = self.output.clone()
-        self.complete.record(current)
-        return output
+    # -- the forward ----------------------------------------------------------------
+    def _encode(self, ops: _Operands, x: torch.Tensor, mask: Optional[torch.Tensor],
+                tally) -> torch.Tensor:
+        """Pre-LN encoder over resolved operands; returns the final normalised output.
+
+        ``x`` carries the residual stream, ``h`` the normalised input of the
+        next sublayer.  Each block's second fused residual + LayerNorm zeroes
+        the invalid rows of the residual stream (the organizer block's
+        masked_fill, benchmark :142-144) and the last one zeroes the invalid
+        rows of the output (benchmark :169-171).  Padded rows never reach a
+        valid row: their keys are masked in every attention and everything
+        else is row-wise.
+        """
+        masked = mask is not None
+        h = layer_norm(x, *ops.entry_norm)
+        last = len(ops.blocks) - 1
+        for index, block in enumerate(ops.blocks):
+            x, h = self._fused_norm(x, self._attend(block, h, mask, tally), block.norm2, mask,
+                                    tally)
+            x, h = self._fused_norm(x, self._feed_forward(block, h), block.exit_norm, mask, tally,
+                                    zero_residual=masked, zero_output=masked and index == last)
+        return h
+
+    def _attend(self, block: _Block, h: torch.Tensor, mask, tally) -> torch.Tensor:
+        batch, seq_len, width = h.shape
+        qkv = F.linear(h, block.qkv_weight, block.qkv_bias)
+        q, k, v = qkv.view(batch, seq_len, 3, block.num_heads, block.head_dim).unbind(2)
+        context, record = attention_forward(q, k, v, mask, causal=self.config.causal,
+                                            scale=block.scale, backend=self.attention_backend)
+        tally.count_attention(record.selected)
+        return F.linear(context.view(batch, seq_len, width), block.out_weight, block.out_bias)
+
+    @staticmethod
+    def _feed_forward(block: _Block, h: torch.Tensor) -> torch.Tensor:
+        inner = gelu_(F.linear(h, block.ffn_in_weight, block.ffn_in_bias))
+        return F.linear(inner, block.ffn_out_weight, block.ffn_out_bias)
+
+    @staticmethod
+    def _fused_norm(x, update, norm: _Norm, mask, tally, *, zero_residual=False,
+                    zero_output=False):
+        pair = fused_residual_layer_norm(x, update, norm.weight, norm.bias, norm.eps, mask,
+                                         zero_invalid_residual=zero_residual,
+                                         zero_invalid_normalized=zero_output)
+        tally.count_fused_norm()
+        return pair
+
+    def _forward_eager(self, x: torch.Tensor,
+                       valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        mask = valid_token_mask
+        if mask is not None and not mask.is_contiguous():
+            mask = mask.contiguous()
+        return self._encode(self._operands(), x.contiguous(), mask, _ModelTally(self))
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self._replay_refusal(x, valid_token_mask) is None:
+            ops = self._operands()
+            if ops.fingerprint is not None:
+                return self._replay_forward(ops, x, valid_token_mask)
+        return self._forward_eager(x, valid_token_mask)
+
+    # -- graph replay -------------------------------------------------------------
+    def _replay_forward(self, ops: _Operands, x, mask) -> torch.Tensor:
+        geometry = (x.device, tuple(x.shape), x.dtype, mask is not None,
+                    torch.is_inference_mode_enabled())
+        cache = self._replay
+        # The lock orders host-side capture and replay; the capture's event
+        # orders its static buffers between caller streams.
+        with cache.lock:
+            captured = cache.entry(
+                (ops.fingerprint, self.attention_backend), geometry,
+                lambda: CapturedForward(lambda xs, ms, t: self._encode(ops, xs, ms, t), x, mask,
+                                        ops.keepalive),
+            )
+            result = captured.replay(x, mask)
+            for selected, count in captured.tally.attention.items():
+                self.attention_backend_counts[selected] = (
+                    self.attention_backend_counts.get(selected, 0) + count)
+            self.fused_residual_layer_norm_calls += captured.tally.fused_norms
+            self.cuda_graph_replays += 1
+        return result
+
+    def _can_replay_cuda_graph(self, x, valid_token_mask) -> bool:
+        return (self._replay_refusal(x, valid_token_mask) is None
+                and self._operands().fingerprint is not None)
+
+    def _replay_refusal(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> Optional[str]:
+        """The first rule that keeps this call eager, or None if it may replay.
+
+        Eligibility follows the reference's (submission.py:561-601) without its
+        measured-shape whitelist: eval-mode inference of a supported dtype on
+        the current ROCm device, no autograd, autocast, compilation, capture
+        in progress or global module hooks; the input must match the model's
+        width, dtype and device.
+        """
+        if self.execution_mode != "auto":
+            return "execution_mode='eager'"
+        if self.attention_backend != "auto":
+            return "attention backend is forced"
+        if self.training:
+            return "training mode"
+        if torch.is_grad_enabled():
+            return "autograd enabled"
+        if not x.is_cuda:
+            return "input not on a ROCm device"
+        if x.ndim != 3 or x.shape[2] != self.config.d_model or x.numel() == 0:
+            return "input is not a non-empty [batch, seq, d_model] tensor"
+        if not x.is_contiguous():
+            return "input not contiguous"
+        if x.dtype not in SUPPORTED_DTYPES:
+            return "unsupported dtype"
+        if x.dtype != self.final_norm.weight.dtype or x.device != self.final_norm.weight.device:
+            return "input dtype or device differs from the model's"
+        if torch.cuda.current_device() != x.device.index:
+            return "input not on the current device"
+        if torch.cuda.is_current_stream_capturing():
+            return "caller is capturing a graph"
+        if torch.is_autocast_enabled("cuda"):
+            return "autocast enabled"
+        if torch.compiler.is_compiling():
+            return "inside torch.compile"
+        if nn.modules.module._global_forward_hooks or nn.modules.module._global_forward_pre_hooks:
+            return "global module hooks registered"
+        if mask is not None and (mask.shape != x.shape[:2] or mask.dtype is not torch.bool
+                                 or mask.device != x.device or not mask.is_contiguous()):
+            return "mask is not a contiguous [batch, seq] bool tensor on the input's device"
+        return None
 
 
 # ---------------------------------------------------------------------------
