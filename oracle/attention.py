@@ -191,7 +191,9 @@ def kernel_rounding_attention(
     * reference exponent ``M = ceil(fl32(max_allowed(s) * c))``, an integer;
     * ``p = fl32(exp2(fl32(s * c - M)))``, then ``P = p`` rounded to the
       input dtype (nearest even);
-    * output ``sum(P v) / sum(p)``; rows without an allowed key are zero.
+    * output ``sum(P v) / sum(P)`` - normalised by the sum of the rounded
+      probabilities, so the weights applied to V sum to one; rows without an
+      allowed key are zero.
 
     Any integer in place of ``M`` gives the same result up to a power of two
     that cancels in the division, so a kernel may move its reference lazily
@@ -221,7 +223,7 @@ def kernel_rounding_attention(
         ref = torch.ceil((m * c).float().double())
         p = torch.exp2((s * c - ref[:, None]).float().double()).float()
         rounded = p.to(q.dtype).double()
-        total = p.double().sum(dim=1, keepdim=True)
+        total = rounded.sum(dim=1, keepdim=True)
         out = torch.matmul(rounded, vh) / total.clamp_min(torch.finfo(torch.float64).tiny)
         results.append(out.masked_fill(~any_allowed[:, None], 0.0))
     stacked = torch.stack(results)
@@ -245,7 +247,7 @@ def brute_force_kernel_rounding_f64(q, k, v, valid_token_mask=None, causal=False
     logits rounded to float32 from float64 dot products, an integer reference
     exponent ``ceil(float32(max * c))``, ``p = float32(2 ** float32(x * c -
     M))``, P rounded to bf16 by its bit pattern (nearest even) or to fp16 by
-    numpy, output ``sum(P v) / sum(p)``.  ``p_dtype`` is "bfloat16",
+    numpy, output ``sum(P v) / sum(P)``.  ``p_dtype`` is "bfloat16",
     "float16" or "float32" (no rounding of P).
     """
     q = np.asarray(q, dtype=np.float64)
@@ -276,6 +278,6 @@ def brute_force_kernel_rounding_f64(q, k, v, valid_token_mask=None, causal=False
                 top = math.ceil(float(np.float32(max(logits) * c)))
                 p = [np.float32(2.0 ** float(np.float32(x * c - top))) for x in logits]
                 weights = [round_p(pi) for pi in p]
-                total = sum(float(pi) for pi in p)
+                total = sum(weights)
                 out[b, s, h] = sum(w * v[b, t, h] for w, t in zip(weights, keys)) / total
     return out

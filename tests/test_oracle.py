@@ -459,8 +459,10 @@ def test_kernel_rounding_oracle_unrounded_is_the_reference_math():
 
 
 def test_p_rounding_error_is_within_its_closed_form_bound():
-    # Rounding P to 8 (bf16) / 11 (fp16) significant bits moves an output by at
-    # most 2^-8 (2^-11) of sum(p |v|) / sum(p) from the unrounded value.
+    # With w_i = p_i (1 + e_i), |e_i| <= u (u = 2^-8 for bf16, 2^-11 for fp16),
+    # sum(w v)/sum(w) - sum(p v)/sum(p) = sum(p_i e_i (v_i - out)) / sum(w),
+    # whose magnitude is at most u/(1-u) * sum(p |v_i - out|) / sum(p)
+    # <= 2u/(1-u) * sum(p |v|) / sum(p).
     for dtype, q, k, v, mask, causal, scale in _rounding_cases():
         rounded = kernel_rounding_attention(q, k, v, mask, causal, scale)
         exact = torch.from_numpy(brute_force_kernel_rounding_f64(
@@ -468,7 +470,8 @@ def test_p_rounding_error_is_within_its_closed_form_bound():
         magnitude = torch.from_numpy(brute_force_kernel_rounding_f64(
             q.float(), k.float(), v.float().abs(), mask, causal, scale, "float32"))
         unit = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
-        assert bool(((rounded - exact).abs() <= unit * magnitude + 1e-12).all())
+        bound = 2 * unit / (1 - unit) * magnitude + 1e-12
+        assert bool(((rounded - exact).abs() <= bound).all())
 
 
 def _mistake_round_normalized_p(q, k, v, mask, causal, scale):
@@ -507,11 +510,37 @@ def _mistake_fractional_reference(q, k, v, mask, causal, scale):
             s = s.masked_fill(~allowed, float("-inf"))
             m = s.max(1).values.nan_to_num(0.0, neginf=0.0)
             p = torch.exp2((s * c - (m * c)[:, None]).float().double()).float()
-            out[b, :, h] = (p.to(q.dtype).double() @ v[b, :, h].double()) / p.double().sum(1, keepdim=True).clamp_min(1e-300)
+            w = p.to(q.dtype).double()
+            out[b, :, h] = (w @ v[b, :, h].double()) / w.sum(1, keepdim=True).clamp_min(1e-300)
     return out
 
 
-@pytest.mark.parametrize("mistake", [_mistake_round_normalized_p, _mistake_fractional_reference])
+def _mistake_unrounded_row_sum(q, k, v, mask, causal, scale):
+    # Normalising by the sum of the unrounded p instead of the rounded P.
+    from oracle.attention import _exp2_scale
+
+    batch, seq_len, heads, head_dim = q.shape
+    sign, c = _exp2_scale(head_dim, scale)
+    out = torch.zeros(q.shape, dtype=torch.float64)
+    for b in range(batch):
+        for h in range(heads):
+            s = (q[b, :, h].double() * sign @ k[b, :, h].double().T).float().double()
+            allowed = torch.ones(seq_len, seq_len, dtype=torch.bool)
+            if causal:
+                allowed = allowed.tril()
+            if mask is not None:
+                allowed &= mask[b][None, :]
+            s = s.masked_fill(~allowed, float("-inf"))
+            m = s.max(1).values.nan_to_num(0.0, neginf=0.0)
+            ref = torch.ceil((m * c).float().double())
+            p = torch.exp2((s * c - ref[:, None]).float().double()).float()
+            w = p.to(q.dtype).double()
+            out[b, :, h] = (w @ v[b, :, h].double()) / p.double().sum(1, keepdim=True).clamp_min(1e-300)
+    return out
+
+
+@pytest.mark.parametrize("mistake", [_mistake_round_normalized_p, _mistake_fractional_reference,
+                                     _mistake_unrounded_row_sum])
 def test_planted_rounding_mistakes_are_caught_by_the_brute_force(mistake):
     worst = 0.0
     for dtype, q, k, v, mask, causal, scale in _rounding_cases():

@@ -105,6 +105,33 @@ __device__ __forceinline__ unsigned short to_bits(F16, float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Sum of the 16-bit probabilities a lane holds for one tile (NP packed u16x8
+// registers of 8 values), accumulated in fp32 with v_dot2c_f32_{bf16,f16}
+// against (1, 1): one instruction per two values, four independent chains.
+// Summing the rounded P that the P.V product uses makes the weights applied
+// to V sum to one exactly in the final division.
+__device__ __forceinline__ float dot2_ones(BF16, unsigned pair, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
+                                         __builtin_bit_cast(bf16x2, 0x3F803F80u), acc, false);
+}
+__device__ __forceinline__ float dot2_ones(F16, unsigned pair, float acc) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, 0x3C003C00u),
+                                acc, false);
+}
+template <typename T, int NP>
+__device__ __forceinline__ float sum_packed(const u16x8 (&pn)[NP]) {
+  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const u32x4 w = __builtin_bit_cast(u32x4, pn[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[j] = dot2_ones(T{}, w[j], part[j]);
+  }
+  return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // Max / sum of a value and the same value in lane ^ 32 (v_permlane32_swap:
@@ -984,6 +1011,32 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       }
     };
 
+    // Copies of a tile that lies wholly before S (no ragged rows): the
+    // (row, chunk) offsets computed once, no per-lane range test.  With whole
+    // 64-lane DMA instructions (BN * KCH and BN * VCH multiples of 64) the only
+    // guard left is the wave-uniform instruction count.
+    static_assert((BN * KCH) % 64 == 0 && (BN * VCH) % 64 == 0, "whole DMA instructions");
+    auto dma_k_full = [&](int buf, int t) __attribute__((always_inline)) {
+      if constexpr (HAS_MASK) {
+        const int key = t * BN + lane;
+        rm = lane < BN && M[key * p.ms] != 0;
+      }
+      const St* kt = K + static_cast<int64_t>(t) * BN * p.ks;
+#pragma unroll
+      for (int i = 0; i < KPW; ++i) {
+        const int j = wave + NW * i;
+        if (j < NK) dma16(kt, koff[i], &smK[buf][512 * j]);
+      }
+    };
+    auto dma_v_full = [&](int buf, int t) __attribute__((always_inline)) {
+      const St* vt = V + static_cast<int64_t>(t) * BN * p.vs;
+#pragma unroll
+      for (int i = 0; i < VPW; ++i) {
+        const int j = wave + NW * i;
+        if (j < NV) dma16(vt, voff[i], &smV[buf][512 * j]);
+      }
+    };
+
     auto kread = [&](int buf, int sb, int g) __attribute__((always_inline)) -> u16x8 {
       const int row = sb * 32 + m;
       return *reinterpret_cast<const u16x8*>(&smK[buf][row * KS + 16 * g + 8 * h]);
@@ -1092,28 +1145,25 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       mt = max_with_other_half(mt);
       rebase(mt);
       const float mc = ceilf(((MASKED && m_run == -INFINITY) ? 0.0f : m_run) * c);
-      float ls = 0.0f;
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float pr = fast_exp2(__builtin_fmaf(s[sb][r], c, -mc));
-          ls += pr;
           pn[sb * 2 + (r >> 3)][r & 7] = to_bits(T{}, pr);
         }
-      l_run += ls;
+      l_run += sum_packed<T>(pn);
     };
 
     // P.V of the pending tile interleaved with the softmax of s: the first
-    // half of the k-steps carries the row max, the second half the exp2 /
-    // running sum / conversion.
-    auto fused = [&](auto masked_tag, int buf, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) {
-      constexpr bool MASKED = decltype(masked_tag)::value;
+    // half of the k-steps carries the row max, the second half the exp2 and
+    // conversion (the steady body of key-masked launches).
+    auto fused = [&](int buf, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) __attribute__((always_inline)) {
       constexpr int HALF = NSTEP / 2;
       constexpr int E = NSB * 16;      // score elements per lane
       constexpr int PER = E / HALF;    // elements per step in each phase
       float mt = -INFINITY;
-      float ls = 0.0f, m_use = 0.0f, alpha = 1.0f, mc = 0.0f;
+      float m_use = 0.0f, alpha = 1.0f, mc = 0.0f;
       bool rebase_any = false;
       u16x8 vr[PDV];
 #pragma unroll
@@ -1139,14 +1189,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
             // key so far) must not turn its zeros into NaN when another row
             // of the wavefront moves.
             alpha = m_use == m_run ? 1.0f : fast_exp2(ceilf(m_run * c) - ceilf(m_use * c));
-            mc = ceilf(((MASKED && m_use == -INFINITY) ? 0.0f : m_use) * c);
+            mc = ceilf((m_use == -INFINITY ? 0.0f : m_use) * c);
           }
         } else {
 #pragma unroll
           for (int j = 0; j < PER; ++j) {
             const int e = PER * (idx - HALF) + j;
             const float pr = fast_exp2(__builtin_fmaf(s[e >> 4][e & 15], c, -mc));
-            ls += pr;
             pn[(e >> 4) * 2 + ((e & 15) >> 3)][e & 7] = to_bits(T{}, pr);
           }
         }
@@ -1158,8 +1207,78 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
         m_run = m_use;
       }
-      l_run += ls;
+      l_run += sum_packed<T>(pn);
     };
+    // Pipelined full tiles (launches without a key mask).  Q.K runs one tile
+    // ahead, so each wavefront has matrix-core work beside its softmax VALU
+    // work in both halves of a tile (Q.K on its own was the longest stretch
+    // of a tile in which the wavefront could issue nothing else):
+    //   phase A: S(t+1) = K(t+1).Q^T, interleaved with the exp2 and 16-bit
+    //            conversion of S(t) into P(t) against the reference mc;
+    //   phase B: O^T += V(t)^T.P(t), interleaved with the row max of S(t+1);
+    //            then the row sum of P(t) and the reference decision for
+    //            tile t+1 (with the accumulator rescale when it moves).
+    auto phase_a = [&](int kbuf, f32x16 (&sn)[NSB], const f32x16 (&s)[NSB], float mc)
+        __attribute__((always_inline)) {
+      constexpr int NQK = G * NSB;  // Q.K MFMAs of a tile
+      constexpr int E = NSB * 16;   // score elements per lane
+      constexpr int PER = E / NQK;  // exp2 per MFMA
+      static_assert(E % NQK == 0, "the softmax work divides over the Q.K steps");
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) sn[sb] = f32x16{};
+      u16x8 kr[PDK][NSB];
+#pragma unroll
+      for (int i = 0; i < PDK && i < G; ++i)
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) kr[i][sb] = kread(kbuf, sb, i);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          sn[sb] = mfma_16(T{}, kr[g % PDK][sb], qf[g], sn[sb]);
+#pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int e = PER * (g * NSB + sb) + j;
+            const float pr = fast_exp2(__builtin_fmaf(s[e >> 4][e & 15], c, -mc));
+            pk[(e >> 4) * 2 + ((e & 15) >> 3)][e & 7] = to_bits(T{}, pr);
+          }
+        }
+        if (g + PDK < G) {
+#pragma unroll
+          for (int sb = 0; sb < NSB; ++sb) kr[g % PDK][sb] = kread(kbuf, sb, g + PDK);
+        }
+        fence();
+      }
+    };
+    // ADD_SUM: whether P(t) still has to enter the row sum (the generic
+    // softmax counts its P when producing it).
+    auto phase_b = [&](auto add_sum_tag, int vbuf, const f32x16 (&sn)[NSB])
+        __attribute__((always_inline)) {
+      constexpr bool ADD_SUM = decltype(add_sum_tag)::value;
+      constexpr int E = NSB * 16;
+      constexpr int PER = E / NSTEP;  // max operands per P.V MFMA
+      static_assert(E % NSTEP == 0, "the row max divides over the P.V steps");
+      float mt = -INFINITY;
+      u16x8 vr[PDV];
+#pragma unroll
+      for (int i = 0; i < PDV && i < NSTEP; ++i) vr[i] = vread(vbuf, i);
+#pragma unroll
+      for (int idx = 0; idx < NSTEP; ++idx) {
+        acc[idx % NDB] = mfma_16(T{}, vr[idx % PDV], pk[idx / NDB], acc[idx % NDB]);
+        if (idx + PDV < NSTEP) vr[idx % PDV] = vread(vbuf, idx + PDV);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int e = PER * idx + j;
+          mt = fmaxf(mt, sn[e >> 4][e & 15]);
+        }
+        fence();
+      }
+      if constexpr (ADD_SUM) l_run += sum_packed<T>(pk);
+      rebase(max_with_other_half(mt));
+    };
+    // Reference exponent of the current tile (without a key mask every row
+    // of a full tile has finite scores after tile 0).
+    auto ref_exp = [&]() __attribute__((always_inline)) -> float { return ceilf(m_run * c); };
 
     dma_k(0, 0);
     vm_wait();
@@ -1211,22 +1330,83 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     };
 
     generic_tile(0);
-    for (int t = 1; t < n_full; ++t) {
-      const int kb = t & 1;
-      if (t + 1 < ntiles) dma_k(kb ^ 1, t + 1);
-      dma_v(kb, t);
-      f32x16 s[NSB];
-      u16x8 pn[NSB * 2];
-      qk(std::false_type{}, kb, NSB, s);
-      if constexpr (HAS_MASK) {
+    if constexpr (HAS_MASK) {
+      // Key-masked launches keep one score buffer (the second one of the
+      // pipelined body costs them an occupancy step at head_dim 64 and
+      // spills at 128, which outweighs the overlap).
+      for (int t = 1; t < n_full; ++t) {
+        const int kb = t & 1;
+        if (t + 1 < n_full) {
+          dma_k_full(kb ^ 1, t + 1);
+        } else if (t + 1 < ntiles) {
+          dma_k(kb ^ 1, t + 1);
+        }
+        dma_v_full(kb, t);
+        f32x16 s[NSB];
+        u16x8 pn[NSB * 2];
+        qk(std::false_type{}, kb, NSB, s);
         apply_mask<NSB, false>(s, t * BN, kvalid, qrow, h);
-        fused(std::true_type{}, kb ^ 1, s, pn);
-      } else {
-        fused(std::false_type{}, kb ^ 1, s, pn);
-      }
+        fused(kb ^ 1, s, pn);
 #pragma unroll
-      for (int i = 0; i < NSB * 2; ++i) pk[i] = pn[i];
-      finish_tile(t);
+        for (int i = 0; i < NSB * 2; ++i) pk[i] = pn[i];
+        finish_tile(t);
+      }
+    } else if (n_full >= 2) {
+      // Every interval between two barriers copies and reads the same buffers
+      // as the generic tile of that index (K(tau+1), V(tau) in; K(tau),
+      // V(tau-1) read), so wavefronts on different paths stay in step.
+      // S(t) lives in sa for odd t and in sb for even t.
+      f32x16 sa[NSB], sb[NSB];
+      // Tile 1: S(1) with nothing to overlap, then P.V(0) with its row max.
+      if (2 < n_full) {
+        dma_k_full(0, 2);
+      } else if (2 < ntiles) {
+        dma_k(0, 2);
+      }
+      dma_v_full(1, 1);
+      qk(std::false_type{}, 1, NSB, sa);
+      phase_b(std::false_type{}, 0, sa);
+      finish_tile(1);
+      // Tile t + 1 for t = 1 .. n_full - 2.
+      auto steady = [&](int t, const f32x16 (&cur)[NSB], f32x16 (&nxt)[NSB])
+          __attribute__((always_inline)) {
+        const int kb = t & 1;
+        if (t + 2 < n_full) {
+          dma_k_full(kb, t + 2);
+        } else if (t + 2 < ntiles) {
+          dma_k(kb, t + 2);
+        }
+        dma_v_full(kb ^ 1, t + 1);
+        phase_a(kb ^ 1, nxt, cur, ref_exp());
+        phase_b(std::true_type{}, kb, nxt);
+        finish_tile(t + 1);
+      };
+      int t = 1;
+      for (; t + 2 < n_full; t += 2) {
+        steady(t, sa, sb);
+        steady(t + 1, sb, sa);
+      }
+      if (t + 1 < n_full) {
+        steady(t, sa, sb);
+        ++t;
+      }
+      // Tile n_full - 1: its P becomes the pending P.V of the next tile.
+      const float mc = ref_exp();
+      auto last_p = [&](const f32x16 (&cur)[NSB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < NSB * 16; ++e) {
+          const float pr = fast_exp2(__builtin_fmaf(cur[e >> 4][e & 15], c, -mc));
+          pk[(e >> 4) * 2 + ((e & 15) >> 3)][e & 7] = to_bits(T{}, pr);
+        }
+      };
+      if (t & 1) {
+        last_p(sa);
+      } else {
+        last_p(sb);
+      }
+      l_run += sum_packed<T>(pk);
+      pending = true;
+      pend_live = NSB;
     }
     for (int t = max(1, n_full); t < ntiles; ++t) generic_tile(t);
     if (pending) pv((ntiles - 1) & 1, pend_live);
