@@ -18,13 +18,14 @@
 #ifndef TTK_HIP_H
 #define TTK_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#define TTK_ABI_VERSION 3
+#define TTK_ABI_VERSION 4
 
 typedef enum {
   TTK_OK = 0,
@@ -77,6 +78,50 @@ ttk_status ttk_attention_fwd(const void* q, const void* k, const void* v,
                              const int64_t mask_strides[2],
                              const int64_t o_strides[3], float scale,
                              int causal, void* stream);
+
+/*
+ * Workspace bytes ttk_attention_fwd_ws uses for this launch on the current
+ * device; 0 when the launch needs none (every launch but a causal bf16/fp16
+ * one whose heaviest query tile outweighs 1.5 average workgroup slots).
+ * Also 0 for arguments ttk_attention_fwd would reject.
+ *
+ * No counterpart in the reference (its Triton launch has no workspace); it
+ * sizes the buffer of the key-split schedule below.
+ */
+size_t ttk_attention_workspace_size(int dtype, int64_t B, int64_t S, int64_t H,
+                                    int64_t D, int causal);
+
+/*
+ * ttk_attention_fwd with a caller-owned workspace (256-byte aligned,
+ * workspace_bytes long).  The workspace starts with the arrival counters of
+ * the schedule, B * H * ceil(S / 128) * 4 bytes rounded up to a multiple of
+ * 256; those must be zero before the first call, and every call leaves them
+ * zero.  The rest needs no initialisation.
+ *
+ * With at least ttk_attention_workspace_size() bytes, a causal bf16/fp16
+ * launch whose heaviest query tile outweighs 1.5 average workgroup slots
+ * cuts each query tile that sees more key tiles than the average slot
+ * carries into key chunks, run as separate workgroups whose partial softmax
+ * states (integer reference exponent, row sum, accumulators) are merged by
+ * the chunk that finishes last - the launch no longer lasts as long as its
+ * heaviest query tile.  With less (or NULL), the call equals
+ * ttk_attention_fwd.  Calls that share a workspace must not overlap (same
+ * stream, or ordered by events).
+ *
+ * Replaces the same launch as ttk_attention_fwd (reference
+ * transformer_opt/kernels/attention.py:306-360); the workspace is this
+ * build's addition.
+ */
+ttk_status ttk_attention_fwd_ws(const void* q, const void* k, const void* v,
+                                const uint8_t* key_valid, void* out, int dtype,
+                                int64_t B, int64_t S, int64_t H, int64_t D,
+                                const int64_t q_strides[3],
+                                const int64_t k_strides[3],
+                                const int64_t v_strides[3],
+                                const int64_t mask_strides[2],
+                                const int64_t o_strides[3], float scale,
+                                int causal, void* workspace,
+                                size_t workspace_bytes, void* stream);
 
 /*
  * Fused residual add + LayerNorm over `rows` contiguous rows of width N:

@@ -733,3 +733,93 @@ def test_config5a_long_sequence_bf16_rows_and_memory(gpu_ready):
         reference = kernel_rounding_attention(q, k, v, None, True, heads=pairs, query_rows=rows)
         actual = torch.stack([result[b, rows, h, :] for b, h in pairs])
         assert contract_failures(actual, reference) == 0, f"rows {rows}"
+
+
+# ------------------------------------------------------------------ key split --
+def _abi_attention(q, k, v, mask, causal, workspace=None):
+    """One launch through the C ABI: ttk_attention_fwd, or ttk_attention_fwd_ws
+    with ``workspace`` (a uint8 device tensor) when given."""
+    from transformer_opt import _native
+    from transformer_opt.kernels.attention import _DTYPE_CODE
+
+    lib = _native.load()
+    out = torch.empty_like(q)
+    B, S, H, D = q.shape
+    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), None if mask is None else mask.data_ptr(),
+            out.data_ptr(), _DTYPE_CODE[q.dtype], B, S, H, D,
+            _native.strides3(q.stride()[:3]), _native.strides3(k.stride()[:3]),
+            _native.strides3(v.stride()[:3]),
+            None if mask is None else _native.strides2(mask.stride()),
+            _native.strides3(out.stride()[:3]), D ** -0.5, 1 if causal else 0]
+    stream = torch.cuda.current_stream().cuda_stream
+    if workspace is None:
+        status = lib.ttk_attention_fwd(*args, stream)
+    else:
+        status = lib.ttk_attention_fwd_ws(*args, workspace.data_ptr(), workspace.numel(), stream)
+    _native.check(status, "attention")
+    return out
+
+
+@pytest.mark.parametrize("batch,seq_len,heads,head_dim,dtype,mask_mode", [
+    (1, 4096, 4, 64, torch.bfloat16, "none"),
+    (1, 1024, 2, 64, torch.float16, "prefix"),
+    (2, 1300, 3, 32, torch.bfloat16, "holes"),
+    (1, 2048, 2, 128, torch.bfloat16, "none"),
+    (1, 777, 5, 16, torch.float16, "none"),
+    (1, 3000, 1, 8, torch.bfloat16, "prefix"),
+])
+def test_key_split_schedule_matches_oracle_and_unsplit_launch(gpu_ready, batch, seq_len, heads,
+                                                              head_dim, dtype, mask_mode):
+    # A causal 16-bit launch with few resident rounds splits its heavy query
+    # tiles into key chunks whose partial states the last chunk merges.  The
+    # split launch, the unsplit one (no workspace) and the oracle agree, the
+    # arrival counters are zero again afterwards and a second split launch is
+    # bitwise identical (the merge sums the chunks in a fixed order).
+    from transformer_opt import _native
+
+    lib = _native.load()
+    nbytes = lib.ttk_attention_workspace_size(1 if dtype == torch.bfloat16 else 2, batch, seq_len,
+                                              heads, head_dim, 1)
+    assert nbytes > 0, "the shape should take the key-split schedule"
+    g = torch.Generator().manual_seed(seq_len + head_dim)
+    shape = (batch, seq_len, heads, head_dim)
+    q, k, v = (torch.randn(shape, generator=g).to(dtype) for _ in range(3))
+    mask = None
+    if mask_mode == "prefix":
+        mask = make_mask("prefix", batch, seq_len)
+    elif mask_mode == "holes":
+        mask = torch.rand(batch, seq_len, generator=g) > 0.2
+        mask[:, 0] = True
+    dev = torch.device("cuda")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    md = None if mask is None else mask.to(dev)
+    workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    with torch.inference_mode():
+        split = _abi_attention(qd, kd, vd, md, True, workspace)
+        again = _abi_attention(qd, kd, vd, md, True, workspace)
+        whole = _abi_attention(qd, kd, vd, md, True)
+    torch.cuda.synchronize()
+    counters = -(-batch * heads * (-(-seq_len // 128)) * 4 // 256) * 256
+    assert int(workspace[:counters].count_nonzero()) == 0
+    assert torch.equal(split, again)
+    reference = oracle(q, k, v, mask, True)
+    assert contract_failures(split.cpu(), reference) == 0
+    assert contract_failures(whole.cpu(), reference) == 0
+
+
+def test_key_split_workspace_rules(gpu_ready):
+    # Too small a workspace runs the unsplit schedule (same result as no
+    # workspace, bitwise); an unaligned one is rejected before any launch.
+    from transformer_opt import _native
+
+    lib = _native.load()
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, 1024, 2, 64, generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    nbytes = lib.ttk_attention_workspace_size(1, 1, 1024, 2, 64, 1)
+    assert nbytes > 0 and lib.ttk_attention_workspace_size(1, 1, 1024, 2, 64, 0) == 0
+    small = torch.zeros(nbytes - 256, dtype=torch.uint8, device="cuda")
+    with torch.inference_mode():
+        assert torch.equal(_abi_attention(q, k, v, None, True, small), _abi_attention(q, k, v, None, True))
+        big = torch.zeros(nbytes + 512, dtype=torch.uint8, device="cuda")
+        with pytest.raises(ValueError, match="256-byte aligned"):
+            _abi_attention(q, k, v, None, True, big[16:])

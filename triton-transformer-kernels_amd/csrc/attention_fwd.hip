@@ -72,6 +72,7 @@
 // element before exp2; P is rounded to the input type (v_cvt_pk_bf16_f32 /
 // v_cvt_f16_f32) for the P.V product; the 16-bit A operand (8 keys of one d)
 // is two transposing 8-byte LDS reads of the row-major V tile.
+#include <algorithm>
 #include <atomic>
 
 #include "ttk_common.h"
@@ -196,6 +197,8 @@ struct Work {
   int q_first;   // query tile of the first pass
   int q_second;  // query tile of the second pass (npass == 2)
   int npass;
+  int chunk;     // key-split grid: chunk of q_first's key tiles (of nchunk)
+  int nchunk;
 };
 
 __device__ __forceinline__ Work work_item(const AttnParams& p, bool causal) {
@@ -213,6 +216,17 @@ __device__ __forceinline__ Work work_item(const AttnParams& p, bool causal) {
   }
   Work w;
   w.bh = bh;
+  w.chunk = 0;
+  w.nchunk = 1;
+  if (causal && p.split) {
+    const unsigned e = p.unit_tab[unit];
+    w.q_first = static_cast<int>(e & 1023u);
+    w.chunk = static_cast<int>((e >> 10) & 7u);
+    w.nchunk = static_cast<int>(e >> 13) + 1;
+    w.q_second = w.q_first;
+    w.npass = 1;
+    return w;
+  }
   if (causal && p.fold) {
     // Folded order: the first half of the units takes the heavy query tiles
     // (descending), the second half the light ones (ascending), so that the
@@ -1280,17 +1294,27 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     // of a full tile has finite scores after tile 0).
     auto ref_exp = [&]() __attribute__((always_inline)) -> float { return ceilf(m_run * c); };
 
-    dma_k(0, 0);
+    // Key tiles [kt0, kt1) of this workgroup: all of the query tile's, or one
+    // chunk of them on the key-split grid.
+    int kt0 = 0, kt1 = ntiles;
+    if (w.nchunk > 1) {
+      const int csz = (ntiles + w.nchunk - 1) / w.nchunk;
+      kt0 = w.chunk * csz;
+      kt1 = min(ntiles, kt0 + csz);
+    }
+
+    dma_k(kt0 & 1, kt0);
     vm_wait();
-    uint64_t kvalid = key_bits(0);
+    uint64_t kvalid = key_bits(kt0);
     __syncthreads();
 
-    // Tiles [0, n_full) of this wavefront are "full": every sub-block live,
-    // no causal or ragged-end masking (a key mask may still apply).  Tiles
-    // [1, n_full) run the branch-free steady body; tile 0 and the tail use
-    // the generic body.  Both execute one barrier per tile, so all
-    // wavefronts meet ntiles barriers.
-    const int n_full = q0 >= S ? 0 : min(min(ntiles, S / BN), CAUSAL ? (q0 + 1) / BN : ntiles);
+    // Tiles before n_full are "full" for this wavefront: every sub-block
+    // live, no causal or ragged-end masking (a key mask may still apply).
+    // Tiles (kt0, n_full) run a branch-free steady body; tile kt0 and the
+    // tail use the generic body.  Every path executes one barrier per tile,
+    // so all wavefronts meet kt1 - kt0 barriers.
+    const int n_full = q0 >= S ? 0
+                               : min(kt1, min(S / BN, CAUSAL ? (q0 + 1) / BN : ntiles));
     bool pending = false;  // a tile's P.V is still to be accumulated (uniform)
     int pend_live = 0;     // its number of live sub-blocks
 
@@ -1304,7 +1328,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       const int kb = t & 1;
       // K(t+1) goes to the buffer K(t-1) used, V(t) to the one V(t-2) used;
       // neither is read in this iteration.
-      if (t + 1 < ntiles) dma_k(kb ^ 1, t + 1);
+      if (t + 1 < kt1) dma_k(kb ^ 1, t + 1);
       dma_v(kb, t);
       const int k0 = t * BN;
       const bool live = q0 < S && (!CAUSAL || k0 <= q0 + 31);
@@ -1329,16 +1353,16 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       finish_tile(t);
     };
 
-    generic_tile(0);
+    generic_tile(kt0);
     if constexpr (HAS_MASK) {
       // Key-masked launches keep one score buffer (the second one of the
       // pipelined body costs them an occupancy step at head_dim 64 and
       // spills at 128, which outweighs the overlap).
-      for (int t = 1; t < n_full; ++t) {
+      for (int t = kt0 + 1; t < n_full; ++t) {
         const int kb = t & 1;
         if (t + 1 < n_full) {
           dma_k_full(kb ^ 1, t + 1);
-        } else if (t + 1 < ntiles) {
+        } else if (t + 1 < kt1) {
           dma_k(kb ^ 1, t + 1);
         }
         dma_v_full(kb, t);
@@ -1351,29 +1375,30 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         for (int i = 0; i < NSB * 2; ++i) pk[i] = pn[i];
         finish_tile(t);
       }
-    } else if (n_full >= 2) {
+    } else if (n_full - kt0 >= 2) {
       // Every interval between two barriers copies and reads the same buffers
       // as the generic tile of that index (K(tau+1), V(tau) in; K(tau),
       // V(tau-1) read), so wavefronts on different paths stay in step.
-      // S(t) lives in sa for odd t and in sb for even t.
+      // S(t) lives in sa when t - kt0 is odd and in sb when it is even.
       f32x16 sa[NSB], sb[NSB];
-      // Tile 1: S(1) with nothing to overlap, then P.V(0) with its row max.
-      if (2 < n_full) {
-        dma_k_full(0, 2);
-      } else if (2 < ntiles) {
-        dma_k(0, 2);
+      const int t1 = kt0 + 1;
+      // Tile t1: S(t1) with nothing to overlap, then P.V(kt0) with its row max.
+      if (t1 + 1 < n_full) {
+        dma_k_full((t1 + 1) & 1, t1 + 1);
+      } else if (t1 + 1 < kt1) {
+        dma_k((t1 + 1) & 1, t1 + 1);
       }
-      dma_v_full(1, 1);
-      qk(std::false_type{}, 1, NSB, sa);
-      phase_b(std::false_type{}, 0, sa);
-      finish_tile(1);
-      // Tile t + 1 for t = 1 .. n_full - 2.
+      dma_v_full(t1 & 1, t1);
+      qk(std::false_type{}, t1 & 1, NSB, sa);
+      phase_b(std::false_type{}, kt0 & 1, sa);
+      finish_tile(t1);
+      // Tile t + 1 for t = t1 .. n_full - 2.
       auto steady = [&](int t, const f32x16 (&cur)[NSB], f32x16 (&nxt)[NSB])
           __attribute__((always_inline)) {
         const int kb = t & 1;
         if (t + 2 < n_full) {
           dma_k_full(kb, t + 2);
-        } else if (t + 2 < ntiles) {
+        } else if (t + 2 < kt1) {
           dma_k(kb, t + 2);
         }
         dma_v_full(kb ^ 1, t + 1);
@@ -1381,7 +1406,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         phase_b(std::true_type{}, kb, nxt);
         finish_tile(t + 1);
       };
-      int t = 1;
+      int t = t1;
       for (; t + 2 < n_full; t += 2) {
         steady(t, sa, sb);
         steady(t + 1, sb, sa);
@@ -1399,7 +1424,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
           pk[(e >> 4) * 2 + ((e & 15) >> 3)][e & 7] = to_bits(T{}, pr);
         }
       };
-      if (t & 1) {
+      if ((t - kt0) & 1) {
         last_p(sa);
       } else {
         last_p(sb);
@@ -1408,8 +1433,89 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       pending = true;
       pend_live = NSB;
     }
-    for (int t = max(1, n_full); t < ntiles; ++t) generic_tile(t);
-    if (pending) pv((ntiles - 1) & 1, pend_live);
+    for (int t = max(kt0 + 1, n_full); t < kt1; ++t) generic_tile(t);
+    if (pending) pv((kt1 - 1) & 1, pend_live);
+
+    if (w.nchunk > 1) {
+      // Key-split query tile: publish this chunk's state - per lane the
+      // integer reference exponent E (-inf for a row with no key yet), the
+      // lane half's row sum and the 16 * NDB accumulator values, stored
+      // lane-major so every access is coalesced - then count the chunk in.
+      // The chunk that arrives last merges all states; E differs between
+      // chunks by integers, so every rescale is an exact power of two.
+      //
+      // Coherence without cache-wide maintenance: the chunks of a tile may
+      // run on different XCDs, whose L2 caches are not coherent, and an
+      // agent-scope fence would write back and invalidate a whole L2 (the
+      // K/V tiles every other workgroup on that XCD streams from).  Instead
+      // only the exchanged words are coherent: the states are written and
+      // read with system-scope relaxed atomics (write-through stores,
+      // cache-bypassing loads), each wavefront waits for its stores to
+      // complete (vmcnt) before the barrier that precedes the counter
+      // increment, and the last chunk reads the states only after its
+      // increment has returned.
+      constexpr int NV = NDB * 16 + 2;  // floats per lane
+      const int slot = w.bh * p.split_tiles + (qb - p.split_q0);
+      float* const base = p.ws_part + static_cast<int64_t>(slot) * p.split_maxch * 4 * NV * 64;
+      auto state = [&](int ch) __attribute__((always_inline)) -> float* {
+        return base + static_cast<int64_t>(ch * 4 + wave) * NV * 64 + lane;
+      };
+      auto put = [](float* a, float v) __attribute__((always_inline)) {
+        __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      };
+      auto get = [](const float* a) __attribute__((always_inline)) -> float {
+        return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      };
+      const float e_own = m_run == -INFINITY ? -INFINITY : ceilf(m_run * c);
+      {
+        float* st = state(w.chunk);
+        put(st, e_own);
+        put(st + 64, l_run);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) put(st + (2 + db * 16 + r) * 64, acc[db][r]);
+      }
+      vm_wait();
+      __syncthreads();
+      int* const counter = &p.ws_cnt[w.bh * p.nq + qb];
+      int* arrival = reinterpret_cast<int*>(&smV[0][0]);  // V buffers are idle now
+      if (tid == 0) {
+        *arrival = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      __syncthreads();
+      if (*arrival != w.nchunk - 1) return;  // another chunk finishes this tile
+      float e_max = -INFINITY;
+      for (int ch = 0; ch < w.nchunk; ++ch) e_max = fmaxf(e_max, ch == w.chunk ? e_own : get(state(ch)));
+      // Sum the chunks in chunk order, so the result does not depend on which
+      // one arrived last.
+      f32x16 own[NDB];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        own[db] = acc[db];
+        acc[db] = f32x16{};
+      }
+      const float l_own = l_run;
+      l_run = 0.0f;
+      for (int ch = 0; ch < w.nchunk; ++ch) {
+        const float* st = state(ch);
+        const float e = ch == w.chunk ? e_own : get(st);
+        const float a = (e == -INFINITY) ? 0.0f : fast_exp2(e - e_max);
+        if (ch == w.chunk) {
+          l_run += a * l_own;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) acc[db] += a * own[db];
+        } else {
+          l_run += a * get(st + 64);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[db][r] += a * get(st + (2 + db * 16 + r) * 64);
+        }
+      }
+      // Ready for the next launch (the launch boundary orders it).
+      if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 
     // Output through LDS: the accumulator layout gives a lane 4 consecutive
     // d of one query per register group, so direct stores would write 16
@@ -1464,8 +1570,77 @@ int device_cu_count() {
   return n;
 }
 
+// Key-split plan of a causal 16-bit launch (see AttnParams::split).  When the
+// heaviest query tile outweighs the average workgroup slot, the launch lasts
+// as long as that workgroup: a query tile that sees more key tiles than the average
+// workgroup slot carries is cut into chunks of at most that many (and at
+// most 8), and all units are dispatched heaviest first.
+struct SplitPlan {
+  bool on = false;
+  int units = 0;
+  int q0 = 0;
+  int maxch = 1;
+  int64_t cnt_bytes = 0;
+  int64_t bytes = 0;
+  unsigned short tab[kMaxSplitUnits] = {};
+};
+
+// Workgroups of the 16-bit kernel resident per CU (registers / LDS).
+int h16_slots_per_cu(int D) { return D >= 128 ? 2 : 3; }
+
+SplitPlan plan_key_split(int dtype, int D, bool causal, int64_t BH, int64_t S) {
+  SplitPlan sp;
+  if (dtype == 0 || !causal || BH <= 0 || S <= 0) return sp;
+  const int64_t nq = (S + kBM - 1) / kBM;
+  if (nq < 2 || nq > 1024) return sp;
+  const int64_t slots = static_cast<int64_t>(device_cu_count()) * h16_slots_per_cu(D);
+  auto tiles = [&](int64_t i) { return (std::min<int64_t>(S, (i + 1) * kBM) + 63) / 64; };
+  int64_t total = 0;
+  for (int64_t i = 0; i < nq; ++i) total += tiles(i);
+  total *= BH;
+  const int64_t limit = std::max<int64_t>(8, (total + slots - 1) / slots);
+  // Split only when the heaviest query tile carries over 1.5x the average
+  // load of a workgroup slot.  Measured on the MI355X: config 4's attention
+  // (B=4, H=16, S=2048, D=64; 1.41x) ran slower split (62.4 -> 66.6 us: the
+  // extra prologues and the state exchange outweigh the shorter tail), as
+  // did B=8, H=16, S=1024 (1.33x); B=1, H=4, S=4096 (11.6x) went 51.9 ->
+  // 35.4 us and B=2, H=4, S=4096 52.3 -> 42.7 us.
+  if (2 * tiles(nq - 1) <= 3 * limit) return sp;
+  struct Unit {
+    int work, q, c, n;
+  };
+  Unit units[kMaxSplitUnits];
+  int nu = 0;
+  int q0 = static_cast<int>(nq);
+  for (int64_t i = nq - 1; i >= 0; --i) {
+    const int64_t t = tiles(i);
+    const int64_t n0 = std::min<int64_t>(8, (t + limit - 1) / limit);
+    const int64_t csz = (t + n0 - 1) / n0;
+    const int64_t n = (t + csz - 1) / csz;  // every chunk non-empty; ceil(t / n) == csz
+    if (n > 1) q0 = static_cast<int>(i);
+    for (int64_t c = 0; c < n; ++c) {
+      if (nu == kMaxSplitUnits) return SplitPlan{};
+      units[nu++] = Unit{static_cast<int>(std::min(t, (c + 1) * csz) - c * csz), static_cast<int>(i),
+                         static_cast<int>(c), static_cast<int>(n)};
+    }
+  }
+  std::stable_sort(units, units + nu, [](const Unit& a, const Unit& b) { return a.work > b.work; });
+  for (int u = 0; u < nu; ++u) {
+    sp.tab[u] = static_cast<unsigned short>(units[u].q | (units[u].c << 10) | ((units[u].n - 1) << 13));
+    if (units[u].q == nq - 1) sp.maxch = units[u].n;
+  }
+  const int64_t nv = ((D + 31) / 32) * 16 + 2;  // floats of partial state per lane
+  const int64_t split_tiles = nq - q0;
+  sp.q0 = q0;
+  sp.units = nu;
+  sp.cnt_bytes = (BH * nq * 4 + 255) / 256 * 256;  // one counter per (batch, head, query tile)
+  sp.bytes = sp.cnt_bytes + BH * split_tiles * sp.maxch * 4 * nv * 64 * 4;
+  sp.on = true;
+  return sp;
+}
+
 template <int D, bool CAUSAL, bool HAS_MASK>
-hipError_t launch_d(int dtype, AttnParams& p, hipStream_t stream) {
+hipError_t launch_d(int dtype, AttnParams& p, void* ws, int64_t ws_bytes, hipStream_t stream) {
   // Causal pairing (fp32 kernel only) halves the grid; use it only while the
   // paired grid still gives every workgroup slot of the GPU (CUs x resident
   // workgroups) one workgroup - below that, the tail of the unpaired grid is
@@ -1483,6 +1658,20 @@ hipError_t launch_d(int dtype, AttnParams& p, hipStream_t stream) {
   // One 64-key tile per head and rows for wavefronts 0-1 only: two heads per
   // workgroup (fp32 non-causal kernels, whose second K/V buffer is free).
   p.twin = (dtype == 0 && !CAUSAL && F32Cfg<D, CAUSAL>::BN == 64 && p.S <= 64) ? 1 : 0;
+  p.split = 0;
+  if (dtype != 0 && CAUSAL && ws != nullptr) {
+    const SplitPlan sp = plan_key_split(dtype, D, true, p.BH, p.S);
+    if (sp.on && ws_bytes >= sp.bytes) {
+      p.split = 1;
+      p.units = sp.units;
+      p.split_q0 = sp.q0;
+      p.split_tiles = p.nq - sp.q0;
+      p.split_maxch = sp.maxch;
+      p.ws_cnt = static_cast<int*>(ws);
+      p.ws_part = reinterpret_cast<float*>(static_cast<char*>(ws) + sp.cnt_bytes);
+      std::copy(sp.tab, sp.tab + sp.units, p.unit_tab);
+    }
+  }
   const unsigned groups = p.twin ? static_cast<unsigned>((p.BH + 1) / 2)
                                  : static_cast<unsigned>(p.units) * static_cast<unsigned>(p.BH);
   const dim3 g(groups), blk(kThreads);
@@ -1496,13 +1685,14 @@ hipError_t launch_d(int dtype, AttnParams& p, hipStream_t stream) {
 }
 
 template <int D>
-hipError_t launch_flags(int dtype, bool causal, bool has_mask, AttnParams& p, hipStream_t stream) {
+hipError_t launch_flags(int dtype, bool causal, bool has_mask, AttnParams& p, void* ws,
+                        int64_t ws_bytes, hipStream_t stream) {
   if (causal) {
-    return has_mask ? launch_d<D, true, true>(dtype, p, stream)
-                    : launch_d<D, true, false>(dtype, p, stream);
+    return has_mask ? launch_d<D, true, true>(dtype, p, ws, ws_bytes, stream)
+                    : launch_d<D, true, false>(dtype, p, ws, ws_bytes, stream);
   }
-  return has_mask ? launch_d<D, false, true>(dtype, p, stream)
-                  : launch_d<D, false, false>(dtype, p, stream);
+  return has_mask ? launch_d<D, false, true>(dtype, p, ws, ws_bytes, stream)
+                  : launch_d<D, false, false>(dtype, p, ws, ws_bytes, stream);
 }
 
 }  // namespace
@@ -1510,15 +1700,20 @@ hipError_t launch_flags(int dtype, bool causal, bool has_mask, AttnParams& p, hi
 int attention_block_m(int /*dtype*/, int /*D*/) { return kBM; }
 
 hipError_t launch_attention(int dtype, int D, bool causal, bool has_mask, AttnParams& p,
-                            hipStream_t stream) {
+                            void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   switch (D) {
-    case 8: return launch_flags<8>(dtype, causal, has_mask, p, stream);
-    case 16: return launch_flags<16>(dtype, causal, has_mask, p, stream);
-    case 32: return launch_flags<32>(dtype, causal, has_mask, p, stream);
-    case 64: return launch_flags<64>(dtype, causal, has_mask, p, stream);
-    case 128: return launch_flags<128>(dtype, causal, has_mask, p, stream);
+    case 8: return launch_flags<8>(dtype, causal, has_mask, p, workspace, workspace_bytes, stream);
+    case 16: return launch_flags<16>(dtype, causal, has_mask, p, workspace, workspace_bytes, stream);
+    case 32: return launch_flags<32>(dtype, causal, has_mask, p, workspace, workspace_bytes, stream);
+    case 64: return launch_flags<64>(dtype, causal, has_mask, p, workspace, workspace_bytes, stream);
+    case 128: return launch_flags<128>(dtype, causal, has_mask, p, workspace, workspace_bytes, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+int64_t attention_workspace_bytes(int dtype, int D, bool causal, int64_t BH, int64_t S) {
+  const SplitPlan sp = plan_key_split(dtype, D, causal, BH, S);
+  return sp.on ? sp.bytes : 0;
 }
 
 }  // namespace ttk

@@ -9,6 +9,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <limits>
 
 #include "ttk_common.h"
@@ -48,13 +49,14 @@ extern "C" int ttk_abi_version(void) { return TTK_ABI_VERSION; }
 
 extern "C" const char* ttk_last_error(void) { return g_error; }
 
-extern "C" ttk_status ttk_attention_fwd(const void* q, const void* k, const void* v,
-                                        const uint8_t* key_valid, void* out, int dtype,
-                                        int64_t B, int64_t S, int64_t H, int64_t D,
-                                        const int64_t q_strides[3], const int64_t k_strides[3],
-                                        const int64_t v_strides[3], const int64_t mask_strides[2],
-                                        const int64_t o_strides[3], float scale, int causal,
-                                        void* stream) {
+namespace {
+
+ttk_status attention_fwd(const void* q, const void* k, const void* v, const uint8_t* key_valid,
+                         void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+                         const int64_t q_strides[3], const int64_t k_strides[3],
+                         const int64_t v_strides[3], const int64_t mask_strides[2],
+                         const int64_t o_strides[3], float scale, int causal, void* workspace,
+                         size_t workspace_bytes, void* stream) {
   g_error[0] = '\0';
   const int es = elem_bytes(dtype);
   if (es == 0) return fail(TTK_EUNSUPPORTED, "attention: unsupported dtype code %d", dtype);
@@ -132,13 +134,51 @@ extern "C" ttk_status ttk_attention_fwd(const void* q, const void* k, const void
   p.scale_log2 = scale * 1.4426950408889634f;
   p.xcd_swizzle = (p.BH % 8 == 0) ? 1 : 0;
 
-  const hipError_t err = ttk::launch_attention(dtype, static_cast<int>(D), causal != 0,
-                                               key_valid != nullptr, p,
-                                               static_cast<hipStream_t>(stream));
+  if (workspace != nullptr && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) {
+    return fail(TTK_EINVAL, "attention: workspace is not 256-byte aligned");
+  }
+  const hipError_t err = ttk::launch_attention(
+      dtype, static_cast<int>(D), causal != 0, key_valid != nullptr, p, workspace,
+      static_cast<int64_t>(std::min<size_t>(workspace_bytes, size_t{1} << 62)),
+      static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     return fail(TTK_ELAUNCH, "attention: launch failed: %s", hipGetErrorString(err));
   }
   return TTK_OK;
+}
+
+}  // namespace
+
+extern "C" ttk_status ttk_attention_fwd(const void* q, const void* k, const void* v,
+                                        const uint8_t* key_valid, void* out, int dtype,
+                                        int64_t B, int64_t S, int64_t H, int64_t D,
+                                        const int64_t q_strides[3], const int64_t k_strides[3],
+                                        const int64_t v_strides[3], const int64_t mask_strides[2],
+                                        const int64_t o_strides[3], float scale, int causal,
+                                        void* stream) {
+  return attention_fwd(q, k, v, key_valid, out, dtype, B, S, H, D, q_strides, k_strides, v_strides,
+                       mask_strides, o_strides, scale, causal, nullptr, 0, stream);
+}
+
+extern "C" size_t ttk_attention_workspace_size(int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+                                               int causal) {
+  if (elem_bytes(dtype) == 0 || B <= 0 || S <= 0 || H <= 0 || B > kMaxGroups || H > kMaxGroups ||
+      (D != 8 && D != 16 && D != 32 && D != 64 && D != 128) || S > (int64_t{1} << 24)) {
+    return 0;
+  }
+  return static_cast<size_t>(
+      ttk::attention_workspace_bytes(dtype, static_cast<int>(D), causal != 0, B * H, S));
+}
+
+extern "C" ttk_status ttk_attention_fwd_ws(const void* q, const void* k, const void* v,
+                                           const uint8_t* key_valid, void* out, int dtype,
+                                           int64_t B, int64_t S, int64_t H, int64_t D,
+                                           const int64_t q_strides[3], const int64_t k_strides[3],
+                                           const int64_t v_strides[3], const int64_t mask_strides[2],
+                                           const int64_t o_strides[3], float scale, int causal,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+  return attention_fwd(q, k, v, key_valid, out, dtype, B, S, H, D, q_strides, k_strides, v_strides,
+                       mask_strides, o_strides, scale, causal, workspace, workspace_bytes, stream);
 }
 
 extern "C" ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u, const void* w,

@@ -95,7 +95,21 @@ struct AttnParams {
   int cu_count;      // compute units of the device (wave-priority phase)
   int twin;          // fp32, S <= 64: two (batch, head) pairs per workgroup
   int fold;          // causal, one resident round: heavy/light query-tile order
+  // Key-split causal grid (16-bit): query tiles heavier than the average
+  // workgroup slot are split into chunks of key tiles; unit u of a (batch,
+  // head) runs query tile unit_tab[u] & 1023, chunk (unit_tab[u] >> 10) & 7
+  // of ((unit_tab[u] >> 13) + 1).  Chunks of query tiles >= split_q0 leave
+  // their partial state in ws_part and count themselves in ws_cnt; the last
+  // one to arrive merges the partials and writes the rows.
+  int split;
+  int split_q0;
+  int split_tiles;   // nq - split_q0
+  int split_maxch;   // chunks of the heaviest query tile
+  int* ws_cnt;       // [BH * nq] arrival counters, zero between launches
+  float* ws_part;    // [BH * split_tiles * split_maxch * 4 waves * lanes * state]
+  unsigned short unit_tab[256];
 };
+constexpr int kMaxSplitUnits = 256;
 
 // Launch parameters of the residual + LayerNorm kernels.
 struct LnParams {
@@ -126,10 +140,16 @@ struct LinearParams {
 };
 
 // Host-side launchers (defined next to their kernels).  Return a HIP error.
-// launch_attention fills p.pair / p.units and sizes the grid itself.
+// launch_attention fills p.pair / p.units / the split plan and sizes the
+// grid itself.  `workspace` (workspace_bytes, 256-byte aligned) may be null;
+// a launch whose split plan needs more than it gets runs unsplit.
 hipError_t launch_attention(int dtype, int D, bool causal, bool has_mask,
-                            AttnParams& p, hipStream_t stream);
+                            AttnParams& p, void* workspace, int64_t workspace_bytes,
+                            hipStream_t stream);
 int attention_block_m(int dtype, int D);
+// Workspace bytes the key-split schedule of this launch uses on the current
+// device (0 when it runs unsplit).
+int64_t attention_workspace_bytes(int dtype, int D, bool causal, int64_t BH, int64_t S);
 
 hipError_t launch_residual_layernorm(int dtype, const LnParams& p, bool vector_path,
                                      int vectors_per_lane, hipStream_t stream);

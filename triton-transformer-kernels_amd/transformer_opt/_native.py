@@ -30,11 +30,13 @@ EXPORTED_SYMBOLS = (
     "ttk_abi_version",
     "ttk_last_error",
     "ttk_attention_fwd",
+    "ttk_attention_workspace_size",
+    "ttk_attention_fwd_ws",
     "ttk_residual_layernorm_fwd",
     "ttk_linear_gelu_fwd",
     "ttk_gelu_fwd",
 )
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -61,6 +63,15 @@ def _configure(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64, _i64,
         _i64p, _i64p, _i64p, _i64p, _i64p,
         ctypes.c_float, ctypes.c_int, _vp,
+    ]
+    lib.ttk_attention_workspace_size.restype = ctypes.c_size_t
+    lib.ttk_attention_workspace_size.argtypes = [ctypes.c_int, _i64, _i64, _i64, _i64, ctypes.c_int]
+    lib.ttk_attention_fwd_ws.restype = ctypes.c_int
+    lib.ttk_attention_fwd_ws.argtypes = [
+        _vp, _vp, _vp, _vp, _vp, ctypes.c_int,
+        _i64, _i64, _i64, _i64,
+        _i64p, _i64p, _i64p, _i64p, _i64p,
+        ctypes.c_float, ctypes.c_int, _vp, ctypes.c_size_t, _vp,
     ]
     lib.ttk_residual_layernorm_fwd.restype = ctypes.c_int
     lib.ttk_residual_layernorm_fwd.argtypes = [

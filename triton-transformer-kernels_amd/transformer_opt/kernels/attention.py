@@ -8,6 +8,7 @@ current stream.  Unsupported inputs raise; nothing falls back.
 
 from __future__ import annotations
 
+import threading
 from typing import Optional
 
 import torch
@@ -25,6 +26,47 @@ _DTYPE_CODE = {
 def hip_available() -> bool:
     """True when a ROCm device is visible and the HIP library loads."""
     return torch.cuda.is_available() and _native.available()
+
+
+_WS_SIZES: dict = {}
+_WORKSPACES: dict = {}
+_WS_LOCK = threading.Lock()
+
+
+def _workspace_bytes(lib, dtype_code: int, batch: int, seq_len: int, heads: int, head_dim: int,
+                     causal: bool, device_index: int) -> int:
+    key = (dtype_code, batch, seq_len, heads, head_dim, causal, device_index)
+    nbytes = _WS_SIZES.get(key)
+    if nbytes is None:
+        nbytes = int(lib.ttk_attention_workspace_size(dtype_code, batch, seq_len, heads, head_dim,
+                                                      1 if causal else 0))
+        _WS_SIZES[key] = nbytes
+    return nbytes
+
+
+def _workspace(device: torch.device, nbytes: int, counter_bytes: int) -> Optional[torch.Tensor]:
+    """Workspace of the key-split attention schedule for the current stream.
+
+    Its arrival counters must be zero before a launch, and every launch
+    leaves them zero.  Outside graph capture each (device, stream) keeps one
+    zero-filled buffer, grown when a launch needs more; launches on one
+    stream never overlap.  During a capture the buffer comes from the
+    graph's memory pool and its counters are cleared inside the graph (a
+    fill kernel, not a memset node), so every replay starts from zero.
+    """
+    if nbytes == 0:
+        return None
+    if torch.cuda.is_current_stream_capturing():
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        ws[:counter_bytes].zero_()
+        return ws
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    with _WS_LOCK:
+        ws = _WORKSPACES.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            _WORKSPACES[key] = ws
+    return ws
 
 
 def _vector_ready(t: torch.Tensor) -> bool:
@@ -81,18 +123,26 @@ def hip_attention(
         mask_ptr = valid_token_mask.data_ptr()
         mask_strides = _native.strides2(valid_token_mask.stride())
 
+    dtype_code = _DTYPE_CODE[q.dtype]
     with torch.cuda.device(q.device):
+        nbytes = _workspace_bytes(lib, dtype_code, batch, seq_len, num_heads, head_dim, causal,
+                                  q.device.index)
+        # The counters lead the workspace: 4 bytes per (batch, head, 128-query
+        # tile), rounded up to 256.
+        counter_bytes = min(nbytes, -(-batch * num_heads * (-(-seq_len // 128)) * 4 // 256) * 256)
+        ws = _workspace(q.device, nbytes, counter_bytes)
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        status = lib.ttk_attention_fwd(
+        status = lib.ttk_attention_fwd_ws(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), mask_ptr, out.data_ptr(),
-            _DTYPE_CODE[q.dtype],
+            dtype_code,
             batch, seq_len, num_heads, head_dim,
             _native.strides3(q.stride()[:3]),
             _native.strides3(k.stride()[:3]),
             _native.strides3(v.stride()[:3]),
             mask_strides,
             _native.strides3(out.stride()[:3]),
-            softmax_scale, 1 if causal else 0, stream,
+            softmax_scale, 1 if causal else 0,
+            None if ws is None else ws.data_ptr(), nbytes, stream,
         )
     _native.check(status, "HIP attention")
     return out
