@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define TTK_ABI_VERSION 4
+#define TTK_ABI_VERSION 5
 
 typedef enum {
   TTK_OK = 0,
@@ -122,6 +122,31 @@ ttk_status ttk_attention_fwd_ws(const void* q, const void* k, const void* v,
                                 const int64_t o_strides[3], float scale,
                                 int causal, void* workspace,
                                 size_t workspace_bytes, void* stream);
+
+/*
+ * ttk_attention_fwd_ws without a caller workspace and without any device
+ * allocation: the key-split schedule keeps its counters and partial states
+ * in a static 32 MiB device array of the library (one per GPU, held until
+ * the process ends), whose address is looked up once per device.  A launch
+ * whose schedule needs more than that (ttk_attention_workspace_size() >
+ * 33554432) is rejected with TTK_EUNSUPPORTED; launches that need no
+ * workspace run as ttk_attention_fwd.  All calls on one GPU share the array:
+ * calls that overlap on one GPU (different streams, unordered) race.  Each
+ * launch leaves the array's counters zero, as they start.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory or pass a workspace: code under hipGraph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.
+ */
+ttk_status ttk_attention_fwd_noalloc(const void* q, const void* k, const void* v,
+                                     const uint8_t* key_valid, void* out, int dtype,
+                                     int64_t B, int64_t S, int64_t H, int64_t D,
+                                     const int64_t q_strides[3],
+                                     const int64_t k_strides[3],
+                                     const int64_t v_strides[3],
+                                     const int64_t mask_strides[2],
+                                     const int64_t o_strides[3], float scale,
+                                     int causal, void* stream);
 
 /*
  * Fused residual add + LayerNorm over `rows` contiguous rows of width N:

@@ -10,7 +10,9 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <atomic>
 #include <limits>
+#include <mutex>
 
 #include "ttk_common.h"
 #include "ttk_hip.h"
@@ -168,6 +170,74 @@ extern "C" size_t ttk_attention_workspace_size(int dtype, int64_t B, int64_t S, 
   }
   return static_cast<size_t>(
       ttk::attention_workspace_bytes(dtype, static_cast<int>(D), causal != 0, B * H, S));
+}
+
+namespace {
+
+// Scratch of ttk_attention_fwd_noalloc: the key-split schedule's counters and
+// partial states live in this static device array instead of a caller's or
+// an allocated workspace.  Every GPU the library runs on holds its own copy
+// from module load until the process ends.  It starts zero-filled, and every
+// launch leaves its counters zero again.
+constexpr size_t kScratchBytes = size_t{32} << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Device address of `scratch` per device.  The array's name is only a
+// host-side handle: kernels and copies get this address, looked up once per
+// device with that device current.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+ttk_status scratch_address(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    return fail(TTK_ELAUNCH, "attention_noalloc: no current device (%s)", hipGetErrorString(err));
+  }
+  void* ptr = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || ptr == nullptr) {
+        return fail(TTK_ELAUNCH, "attention_noalloc: scratch address lookup failed: %s",
+                    hipGetErrorString(err));
+      }
+      g_scratch_addr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return TTK_OK;
+}
+
+}  // namespace
+
+extern "C" ttk_status ttk_attention_fwd_noalloc(const void* q, const void* k, const void* v,
+                                                const uint8_t* key_valid, void* out, int dtype,
+                                                int64_t B, int64_t S, int64_t H, int64_t D,
+                                                const int64_t q_strides[3],
+                                                const int64_t k_strides[3],
+                                                const int64_t v_strides[3],
+                                                const int64_t mask_strides[2],
+                                                const int64_t o_strides[3], float scale,
+                                                int causal, void* stream) {
+  g_error[0] = '\0';
+  const size_t need = ttk_attention_workspace_size(dtype, B, S, H, D, causal);
+  if (need > kScratchBytes) {
+    return fail(TTK_EUNSUPPORTED,
+                "attention_noalloc: this launch's key-split schedule needs %zu bytes of scratch, "
+                "above the static maximum of %zu bytes (use ttk_attention_fwd_ws)",
+                need, kScratchBytes);
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const ttk_status st = scratch_address(&ws);
+    if (st != TTK_OK) return st;
+  }
+  return attention_fwd(q, k, v, key_valid, out, dtype, B, S, H, D, q_strides, k_strides, v_strides,
+                       mask_strides, o_strides, scale, causal, ws, need > 0 ? kScratchBytes : 0, stream);
 }
 
 extern "C" ttk_status ttk_attention_fwd_ws(const void* q, const void* k, const void* v,

@@ -32,11 +32,12 @@ EXPORTED_SYMBOLS = (
     "ttk_attention_fwd",
     "ttk_attention_workspace_size",
     "ttk_attention_fwd_ws",
+    "ttk_attention_fwd_noalloc",
     "ttk_residual_layernorm_fwd",
     "ttk_linear_gelu_fwd",
     "ttk_gelu_fwd",
 )
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -73,6 +74,8 @@ def _configure(lib: ctypes.CDLL) -> None:
         _i64p, _i64p, _i64p, _i64p, _i64p,
         ctypes.c_float, ctypes.c_int, _vp, ctypes.c_size_t, _vp,
     ]
+    lib.ttk_attention_fwd_noalloc.restype = ctypes.c_int
+    lib.ttk_attention_fwd_noalloc.argtypes = lib.ttk_attention_fwd.argtypes
     lib.ttk_residual_layernorm_fwd.restype = ctypes.c_int
     lib.ttk_residual_layernorm_fwd.argtypes = [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int,
