@@ -129,6 +129,30 @@ def test_model_constructor_validation_and_state_surface():
     assert not any("packed" in key for key in keys)
 
 
+def test_model_is_freed_without_the_cyclic_collector():
+    # The operand layout cached in the model's replay cache must not refer
+    # back to the model: a model in a reference cycle is freed only by the
+    # cyclic collector, which may run inside another model's graph capture
+    # and there destroy this model's captured graphs (not allowed during a
+    # capture; the error aborts the process).
+    import gc
+    import weakref
+
+    cfg = TransformerConfig(1, 16, 32, 2, 64, 2, False)
+    model = UserOptimizedTransformer(cfg).eval()
+    ops = model._operands()
+    assert ops.fingerprint is not None and model._replay.layout is not None
+    ref = weakref.ref(model)
+    collecting = gc.isenabled()
+    gc.disable()
+    try:
+        del model, ops
+        assert ref() is None, "the model survived its last reference (reference cycle)"
+    finally:
+        if collecting:
+            gc.enable()
+
+
 def test_model_forward_on_cpu_fails_loudly():
     cfg = TransformerConfig(1, 16, 32, 2, 64, 1, False)
     model = UserOptimizedTransformer(cfg).eval()

@@ -23,6 +23,7 @@ device or dtype move drops every capture.
 
 from __future__ import annotations
 
+import gc
 import threading
 from collections import OrderedDict
 from typing import Callable, Dict, Hashable, Optional, Sequence
@@ -135,8 +136,20 @@ class CapturedForward:
                 run(self.x, self.mask, CallTally())
                 self.tally = CallTally()
                 self.graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(self.graph, stream=side):
-                    self.out = run(self.x, self.mask, self.tally)
+                # No cyclic garbage collection during the capture: garbage
+                # that holds another capture (a dropped model in a reference
+                # cycle) would destroy its graph and release its memory pool
+                # while this stream captures, which HIP does not allow; the
+                # error inside that destructor aborts the process.  torch
+                # does not collect before a capture by default.
+                collecting = gc.isenabled()
+                gc.disable()
+                try:
+                    with torch.cuda.graph(self.graph, stream=side):
+                        self.out = run(self.x, self.mask, self.tally)
+                finally:
+                    if collecting:
+                        gc.enable()
             caller.wait_stream(side)
         # Recorded on the stream of the most recent replay; the next replay,
         # on whatever stream, waits for it before touching the static buffers.

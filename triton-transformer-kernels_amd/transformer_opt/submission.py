@@ -100,7 +100,12 @@ class _Layout:
     ``slots`` holds one ``(dict, key, object)`` triple per edge the forward
     walks - child modules and parameters - so ``intact()`` is a single
     identity pass.  ``tensors`` are the parameters whose stamps key a
-    capture; ``modules`` those whose training flag and hooks do.
+    capture; ``modules`` the submodules whose training flag and hooks do (the
+    root's are read from the model itself: the layout lives in the model's
+    replay cache, and a reference back to the model would make a cycle that
+    only the cyclic garbage collector frees - possibly in the middle of
+    another model's graph capture, where destroying this model's captured
+    graphs is not allowed).
     """
 
     __slots__ = ("epoch", "slots", "modules", "tensors", "norms", "attentions", "layers",
@@ -108,7 +113,7 @@ class _Layout:
 
     def __init__(self, model: "UserOptimizedTransformer", epoch: int) -> None:
         self.epoch = epoch
-        slots, modules, tensors = [], [model], []
+        slots, modules, tensors = [], [], []
 
         def child(parent: nn.Module, name: str) -> nn.Module:
             module = parent._modules[name]
@@ -276,7 +281,7 @@ class UserOptimizedTransformer(nn.Module):
             stamps = None
         scalars = layout.scalars()
         settled = not any(m.training or m._forward_hooks or m._forward_pre_hooks
-                          for m in layout.modules)
+                          for m in (self,) + layout.modules)
         key = (layout.epoch, stamps, scalars)
         ops = cache.operands
         if ops is None or stamps is None or cache.operands_key != key:
