@@ -606,6 +606,35 @@ def test_twin_grid_short_sequences(gpu_ready, batch, seq_len, heads, head_dim, m
         assert bool((actual[0] == 0).all())
 
 
+@pytest.mark.parametrize("batch,seq_len,heads,head_dim,mask_mode,layout", [
+    (512, 64, 8, 64, "none", "packed"),    # config 5b: 8192 items, 4 per wavefront
+    (64, 40, 41, 32, "none", "contiguous"),  # ragged S, items not a multiple of the grid
+    (96, 32, 23, 64, "none", "bhsd"),      # S = 32: one 32-query half per head
+    (40, 9, 61, 64, "prefix", "packed"),   # S < 32 with key masks
+    (33, 64, 65, 32, "holes", "bhsd"),
+])
+def test_short_sequence_persistent_grid(gpu_ready, batch, seq_len, heads, head_dim, mask_mode, layout):
+    # fp32 non-causal S <= 64 with head_dim 32 / 64: one wavefront per (batch,
+    # head, 32-query half), operands loaded straight into registers, a
+    # persistent grid whose wavefronts walk several items and prefetch the
+    # next one.  Every head against the oracle; a second call must agree
+    # bitwise (the schedule is static).
+    rng = torch.Generator().manual_seed(batch * 7 + seq_len * 3 + heads + head_dim)
+    q, k, v = _layout_inputs((batch, seq_len, heads, head_dim), layout, rng)
+    if mask_mode == "holes":
+        mask = torch.rand(batch, seq_len, generator=rng) > 0.4
+        mask[1, :] = False
+    else:
+        mask = make_mask(mask_mode, batch, seq_len)
+    actual = run_hip(q, k, v, mask, False)
+    reference = oracle(q.cpu(), k.cpu(), v.cpu(), mask, False)
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, torch.float32)
+    assert torch.equal(run_hip(q, k, v, mask, False), actual)
+    if mask_mode == "holes":
+        assert bool((actual[1] == 0).all())
+
+
 def test_twin_grid_config5b_shape_with_padding(gpu_ready):
     # Config 5b's attention (fp32, B=512, S=64, H=8, D=64, non-causal) with
     # right padding of every length 1..64 and random holes, every head

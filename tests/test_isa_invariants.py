@@ -53,3 +53,41 @@ def test_m0_is_only_written_by_the_inline_copies(tmp_path, name):
             outside += 1
     assert inside > 0, "expected the inline LDS-DMA copies to write m0"
     assert outside == 0, f"{outside} compiler-generated instructions use m0 in {name}"
+
+
+def test_short_kernel_buffer_offsets_keep_rows_in_the_range_check(tmp_path):
+    # The fp32 short-sequence kernels read rows past S as zeros (and drop
+    # stores to them) through the buffer range check, which covers the VGPR
+    # offset and the instruction offset but not soffset.  That holds only
+    # while every soffset is a column offset inside one row: 0, an inline
+    # constant, or an SGPR set from an immediate below 256 bytes (a head_dim
+    # 64 row).  Any row-dependent soffset would let a row past S through.
+    text = _assembly(CSRC / "attention_fwd.hip", tmp_path)
+    lines = text.splitlines()
+    starts = [i for i, line in enumerate(lines)
+              if line.startswith("_Z") and "short_kernel" in line.split(":")[0] and ":" in line]
+    assert len(starts) == 6, "expected six short-kernel instantiations"
+    checked = 0
+    for start in starts:
+        end = next(i for i in range(start, len(lines)) if lines[i].startswith(".Lfunc_end"))
+        body = [line.split(";")[0].strip() for line in lines[start:end]]
+        for i, ins in enumerate(body):
+            if not ins.startswith("buffer_"):
+                continue
+            ops = ins.replace(",", " ").split()
+            soffset = ops[4]
+            checked += 1
+            if soffset.lstrip("-").isdigit():
+                assert 0 <= int(soffset) < 256, ins
+                continue
+            assert soffset.startswith("s") and soffset[1:].isdigit(), ins
+            # The latest write to that SGPR before this instruction.
+            for j in range(i - 1, -1, -1):
+                words = body[j].replace(",", " ").split()
+                if len(words) >= 2 and words[0].startswith("s_") and words[1] == soffset:
+                    assert words[0] in ("s_mov_b32", "s_movk_i32"), f"{ins} <- {body[j]}"
+                    assert 0 <= int(words[2], 0) < 256, f"{ins} <- {body[j]}"
+                    break
+            else:
+                raise AssertionError(f"no definition of {soffset} before {ins}")
+    assert checked > 0

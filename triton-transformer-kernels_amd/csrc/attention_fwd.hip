@@ -836,6 +836,277 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
 }
 
 // ----------------------------------------------------------------------------
+// fp32, short sequences: S <= 64, non-causal, head_dim 32 / 64
+// ----------------------------------------------------------------------------
+// The whole 64-key tile of one (batch, head) fits a wavefront's registers as
+// MFMA operands (head_dim 64: K 64 + V 64 + Q 32 VGPRs), so one wavefront
+// serves one (batch, head, 32-query half) on its own: no barrier.  The grid
+// is persistent (two workgroups per CU); wavefront gw walks the items gw,
+// gw + W, ... (item = 2 * (batch * H + head) + half, so the two halves of a
+// head run side by side in one workgroup and the second K/V read hits L2).
+// While the current item's softmax and P.V run, the next item's K and Q are
+// in flight, and the next V while the current rows are stored.
+//
+// Global traffic is row-coalesced: K, Q and O move as whole rows (64 lanes x
+// 16 bytes = 1 KB of consecutive rows per instruction) and are re-laid out
+// through an LDS region private to the wavefront (64 rows, 16 KB at head_dim
+// 64; 16-byte chunks XOR-swizzled by row so both layouts access LDS without
+// bank conflicts): K and Q into the MFMA operand layout (key or query per lane,
+// 4 head dims per register), O back from the accumulator layout.  The MFMA
+// fragments read with a lane stride of a whole row (32 rows x 32 bytes per
+// instruction) cost ~8 % more time at config 5b than whole rows.  V is read
+// straight into its operand layout, 256 contiguous bytes per half-wavefront.
+// Fragment layouts, accumulation order and softmax are those of
+// attn_fwd_f32_kernel's single-tile pass, so the two kernels give identical
+// results.
+// MASKED: scores need the key mask (HAS_MASK, or S < 64 leaves padded keys).
+template <int D, bool HAS_MASK, bool MASKED>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_short_kernel(AttnParams p) {
+  static_assert(D == 32 || D == 64, "short-sequence kernel: head_dim 32 or 64");
+  constexpr int NSB = 2, DB = D / 32, G = D / 8;
+  constexpr int CPR = D / 4;        // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;     // rows per row-coalesced instruction
+  constexpr int NI = 32 / RPI;      // instructions per 32 rows (== G)
+  static_assert(NI == G, "32 rows take as many instructions as Q has fragments");
+  using VF = typename VFrag32<D>::type;
+  __shared__ __attribute__((aligned(16))) float smem[kThreads / 64][64 * D];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = lane & 31;
+  const int h = lane >> 5;
+  const int S = p.S;
+  const int hshift = S > 32 ? 1 : 0;  // 32-query halves per head: 2 or 1
+  const int items = p.BH << hshift;
+  const int stride = static_cast<int>(gridDim.x) * (kThreads / 64);
+  int item = static_cast<int>(blockIdx.x) * (kThreads / 64) + wave;
+  if (item >= items) return;
+  float* const region = smem[wave];
+
+  // Every global access is a buffer access whose resource covers exactly the
+  // rows < S of one head (the host checks row stride >= head_dim and that
+  // offsets stay below 2^31): rows past S read as zeros and are not written,
+  // without a branch.  The range check covers the VGPR offset (plus the
+  // instruction offset) but not soffset, so the row part of every offset is
+  // in the VGPR.  The loads of the next item are issued unconditionally -
+  // after the last item with an empty resource, which fetches nothing - so
+  // every wait count is exact on the one path through the loop and waits only
+  // for the operands it needs.
+  auto head_of = [&](int it, int& b, int& hh) {
+    const int bh = it >> hshift;
+    b = bh / p.H;
+    hh = bh - b * p.H;
+  };
+  auto rsrc = [&](const void* base, int64_t bo, int64_t ho, int64_t rs, int it, bool live) {
+    int b, hh;
+    head_of(it, b, hh);
+    const float* ptr = static_cast<const float*>(base) + b * bo + hh * ho;
+    const int bytes = live ? static_cast<int>(((S - 1) * rs + D) * 4) : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ptr), static_cast<short>(0), bytes, 0x00020000);
+  };
+  // Row-coalesced lane position: instruction j covers rows RPI*j .. RPI*j + RPI - 1.
+  const int crow = lane / CPR;
+  const int cchunk = lane % CPR;
+  // LDS float index of (row, 16-byte chunk) in the wavefront's region.
+  auto slot = [](int row, int chunk) { return row * D + 4 * (chunk ^ (row & (CPR - 1))); };
+  const int voff0 = static_cast<int>((4 * h * p.vs + DB * m) * 4);
+
+  f32x4 kst[NSB][NI], qst[NI];  // K and Q as loaded (row-coalesced)
+  VF vf[NSB][16];
+  int key_ok = 0;  // HAS_MASK: this lane's key (= lane) exists and is not masked
+
+  // 32 rows from row0 of one head, row-coalesced (the row offsets of the
+  // instructions are added at each load, not hoisted into live registers).
+  auto load_rows = [&](f32x4 (&dst)[NI], const __amdgpu_buffer_rsrc_t& rs, int64_t row_stride, int row0) {
+    int off = static_cast<int>(((row0 + crow) * row_stride + 4 * cchunk) * 4);
+    asm volatile("" : "+v"(off));
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      dst[j] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + static_cast<int>(RPI * j * row_stride * 4), 0, 0));
+    }
+  };
+  auto load_q = [&](int it, bool live) {
+    const auto rq = rsrc(p.q, p.qb, p.qh, p.qs, it, live);
+    load_rows(qst, rq, p.qs, (it & hshift) << 5);
+    if constexpr (HAS_MASK) {
+      int b, hh;
+      head_of(it, b, hh);
+      const int bytes = live ? static_cast<int>((S - 1) * p.ms + 1) : 0;
+      const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.mask + b * p.mb),
+                                                        static_cast<short>(0), bytes, 0x00020000);
+      key_ok = __builtin_amdgcn_raw_buffer_load_b8(rm, static_cast<int>(lane * p.ms), 0, 0);
+    }
+  };
+  auto load_k = [&](int it, bool live, int sb) {
+    const auto rk = rsrc(p.k, p.kb, p.kh, p.ks, it, live);
+    load_rows(kst[sb], rk, p.ks, sb * 32);
+  };
+  // V as the A operand of O^T += V^T . P^T: register (sb, r) holds key
+  // sb * 32 + acc_row(r, h), head dims DB * m .. DB * m + DB - 1.  The
+  // per-register row offsets are added at each load (an opaque copy of the
+  // lane offset keeps them from being hoisted into 32 live registers).
+  auto load_v = [&](int it, bool live, int sb) {
+    const auto rv = rsrc(p.v, p.vb, p.vh, p.vs, it, live);
+    int voff = voff0;
+    asm volatile("" : "+v"(voff));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int off = voff + static_cast<int>((sb * 32 + acc_row(r, 0)) * p.vs * 4);
+      if constexpr (DB == 1) {
+        vf[sb][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+      } else {
+        vf[sb][r] = __builtin_bit_cast(VF, __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0));
+      }
+    }
+  };
+  // Row-coalesced registers -> LDS region rows row0 .. row0 + 31.
+  auto put_rows = [&](const f32x4 (&src)[NI], int row0) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) *reinterpret_cast<f32x4*>(&region[slot(row0 + RPI * j + crow, cchunk)]) = src[j];
+  };
+  // MFMA operand fragments from the region: group g of lane (m, h) holds row
+  // row0 + m, head dims 8g + 4h .. 8g + 4h + 3 (16-byte chunk 2g + h).
+  auto get_frags = [&](f32x4 (&dst)[G], int row0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) dst[g] = *reinterpret_cast<const f32x4*>(&region[slot(row0 + m, 2 * g + h)]);
+  };
+
+  // Same memory-instruction sequence as the loop body issues before its head
+  // (K, Q, NI row stores, V; the stores here go to an empty resource and
+  // write nothing): vmcnt counts loads and stores together, so the wait
+  // counts the compiler derives at the loop head then fit both paths into it
+  // and none of them waits for the previous item's stores.
+  load_k(item, true, 0);
+  load_k(item, true, 1);
+  load_q(item, true);
+  {
+    const auto none = __builtin_amdgcn_make_buffer_rsrc(p.out, static_cast<short>(0), 0, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, none, 16 * j, 0, 0);
+  }
+  load_v(item, true, 0);
+  load_v(item, true, 1);
+  while (true) {
+    const int next_raw = item + stride;
+    const bool more = next_raw < items;
+    const int next = more ? next_raw : item;
+    const int half_row0 = (item & hshift) << 5;
+    const int qrow = half_row0 + m;
+    const uint64_t kv = HAS_MASK ? __builtin_amdgcn_ballot_w64(lane < S && key_ok != 0) : range_bits(0, S);
+    const auto ro = [&] {
+      int b, hh;
+      head_of(item, b, hh);
+      float* ptr = static_cast<float*>(p.out) + b * p.ob + hh * p.oh;
+      const int bytes = static_cast<int>(((S - 1) * p.os + D) * 4);
+      return __builtin_amdgcn_make_buffer_rsrc(ptr, static_cast<short>(0), bytes, 0x00020000);
+    }();
+
+    // ---- S^T = K . Q^T (sub-block by sub-block; each accumulates over d in
+    // the same order as the tiled kernel).  Q, then K, passes through the LDS
+    // region; one wavefront's LDS accesses complete in program order, so the
+    // K rows overwrite Q's only after Q's fragments are read.
+    f32x4 qf[G];
+    put_rows(qst, 0);
+    get_frags(qf, 0);
+    put_rows(kst[0], 0);
+    put_rows(kst[1], 32);
+#pragma unroll
+    for (int g = 0; g < G; ++g) qf[g] *= p.scale_log2;
+    f32x16 s[NSB];
+    f32x4 kf[NSB][G];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) get_frags(kf[sb], 32 * sb);
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+      s[sb] = f32x16{};
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kf[sb][g][e], qf[g][e], s[sb]);
+    }
+    fence();
+    // The staging registers of K are free since its rows went to LDS.
+    load_k(next, more, 0);
+    load_k(next, more, 1);
+    fence();
+
+    // ---- softmax (exp2 domain, one tile: the running state starts empty) ----
+    if constexpr (MASKED) apply_mask<NSB, false>(s, 0, kv, qrow, h);
+    float mt = s[0][0];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
+    mt = fmaxf(-INFINITY, max_with_other_half(mt));
+    // A fully masked row keeps m = -inf; use 0 so exp2(-inf - 0) = 0, never NaN.
+    const float m_use = (MASKED && mt == -INFINITY) ? 0.0f : mt;
+    float ls = 0.0f;
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(s[sb][r] - m_use);
+        s[sb][r] = pr;
+        ls += pr;
+      }
+    fence();
+
+    // ---- O^T = V^T . P^T ----------------------------------------------------
+    f32x16 acc[DB];
+#pragma unroll
+    for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = s[sb][r];
+        if constexpr (DB == 1) {
+          acc[0] = mfma_f32(vf[sb][r], pr, acc[0]);
+        } else {
+          acc[0] = mfma_f32(vf[sb][r].x, pr, acc[0]);
+          acc[1] = mfma_f32(vf[sb][r].y, pr, acc[1]);
+        }
+      }
+      fence();
+    }
+    load_q(next, more);
+    fence();
+
+    // ---- O = acc / l, through the LDS region into whole rows -----------------
+    const float lt = sum_with_other_half(ls);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4) {
+      // Block i holds d = DB * row + i; register 4 * j4 + e holds row 8 * j4 + 4h + e,
+      // so a lane's d-values for one j4 form one run of 4 * DB (chunks d0 / 4 ..).
+      const int d0 = DB * (8 * j4 + 4 * h);
+      float vals[4 * DB];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < DB; ++i) vals[DB * e + i] = acc[i][4 * j4 + e] * inv;
+#pragma unroll
+      for (int c = 0; c < DB; ++c) {
+        *reinterpret_cast<f32x4*>(&region[slot(m, d0 / 4 + c)]) =
+            f32x4{vals[4 * c], vals[4 * c + 1], vals[4 * c + 2], vals[4 * c + 3]};
+      }
+    }
+    const int ooff = static_cast<int>(((half_row0 + crow) * p.os + 4 * cchunk) * 4);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const f32x4 o4 = *reinterpret_cast<const f32x4*>(&region[slot(RPI * j + crow, cchunk)]);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o4), ro,
+                                             ooff + static_cast<int>(RPI * j * p.os * 4), 0, 0);
+    }
+    fence();
+    load_v(next, more, 0);
+    load_v(next, more, 1);
+    if (!more) break;
+    item = next;
+  }
+}
+
+// ----------------------------------------------------------------------------
 // bf16 / fp16
 // ----------------------------------------------------------------------------
 template <int D>
@@ -1670,6 +1941,29 @@ hipError_t launch_d(int dtype, AttnParams& p, void* ws, int64_t ws_bytes, hipStr
       p.ws_cnt = static_cast<int*>(ws);
       p.ws_part = reinterpret_cast<float*>(static_cast<char*>(ws) + sp.cnt_bytes);
       std::copy(sp.tab, sp.tab + sp.units, p.unit_tab);
+    }
+  }
+  if constexpr (!CAUSAL && (D == 32 || D == 64)) {
+    // Its buffer resources span rows 0..S-1 of one head: rows must not
+    // overlap (sequence stride >= head_dim) and the span must stay below 2^31
+    // bytes, or rows past S would not read as zeros.
+    auto span_ok = [&](int64_t rs) { return rs >= D && ((p.S - 1) * rs + D) * 4 < (int64_t{1} << 31); };
+    if (dtype == 0 && p.S <= 64 && span_ok(p.qs) && span_ok(p.ks) && span_ok(p.vs) && span_ok(p.os) &&
+        (p.S - 1) * p.ms < (int64_t{1} << 31) - 1) {
+      // Short sequences: one wavefront per (batch, head, 32-query half), a
+      // persistent grid of two workgroups per CU (fewer when there are fewer
+      // items than wavefronts).
+      const int64_t items = static_cast<int64_t>(p.BH) * (p.S > 32 ? 2 : 1);
+      const int64_t full = static_cast<int64_t>(p.cu_count) * 2;
+      const int64_t groups = std::min<int64_t>((items + 3) / 4, full);
+      if (HAS_MASK || p.S < 64) {
+        attn_fwd_f32_short_kernel<D, HAS_MASK, true>
+            <<<dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, stream>>>(p);
+      } else {
+        attn_fwd_f32_short_kernel<D, false, false>
+            <<<dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, stream>>>(p);
+      }
+      return hipGetLastError();
     }
   }
   const unsigned groups = p.twin ? static_cast<unsigned>((p.BH + 1) / 2)
