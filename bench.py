@@ -319,8 +319,6 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
                     per-kernel split
     encoder_5b:     config-5b encoder forward (fp32, B=512, S=64, d=512, 4 layers,
                     hipGraph replay), for the per-kernel split
-    linear_gelu:    fused Linear + exact GELU, bf16, the config-4 FFN input projection
-                    (tokens 8192, 1024 -> 4096)
     gelu:           exact GELU, bf16, the config-4 FFN activation [8192, 4096] (GB/s)
     layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
                     among input sets that together exceed twice the 256 MB MALL
@@ -383,14 +381,6 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
             fused_residual_layer_norm(x, u, w, b, 1e-5)
 
         work = layer_norm_bytes(rows, width, elem=2)
-    elif which == "linear_gelu":
-        from transformer_opt.kernels import linear_gelu
-
-        x = torch.randn(8192, 1024, device="cuda").to(torch.bfloat16)
-        w = (torch.randn(4096, 1024, device="cuda") * 1024 ** -0.5).to(torch.bfloat16)
-        b = (torch.randn(4096, device="cuda") * 0.1).to(torch.bfloat16)
-        fn = lambda: linear_gelu(x, w, b)  # noqa: E731
-        work = 2.0 * 8192 * 4096 * 1024
     elif which == "gelu":
         from transformer_opt.kernels import gelu_
 
@@ -464,7 +454,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "layernorm_bf16", "copy", "attention_bf16",
                                                    "attention_bf16_d64", "attention_5b", "encoder_fp32", "encoder_bf16",
-                                                   "encoder_5b", "linear_gelu", "gelu"),
+                                                   "encoder_5b", "gelu"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")

@@ -1,6 +1,6 @@
 /*
  * ttk_hip.h - C ABI of the MI355X (gfx950) fused attention, fused
- * residual-add + LayerNorm, fused Linear + GELU and exact-GELU kernels.
+ * residual-add + LayerNorm and exact-GELU kernels.
  *
  * Plain C: no HIP, no torch types.  Every tensor is a raw device pointer plus
  * element strides.  The caller owns all memory (inputs and outputs); the
@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define TTK_ABI_VERSION 5
+#define TTK_ABI_VERSION 6
 
 typedef enum {
   TTK_OK = 0,
@@ -180,31 +180,6 @@ ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u,
                                       float eps, int zero_invalid_residual,
                                       int zero_invalid_normalized,
                                       void* stream);
-
-/*
- * Fused Linear + exact GELU (the encoder's FFN input projection):
- *
- *   y[m, n] = gelu( sum_k x[m, k] * w[n, k] + bias[n] ),
- *   gelu(v) = 0.5 * v * (1 + erf(v / sqrt(2)))
- *
- * x: [M, K], w: [N, K] (the nn.Linear weight), y: [M, N], all row-major with
- * element row strides ldx, ldw, ldy; bias: N elements or NULL.  dtype is
- * TTK_BF16 or TTK_F16 (fp32 stays on the library GEMM: TTK_EUNSUPPORTED).  The
- * sum accumulates in fp32; bias and GELU act on the fp32 value, which is
- * rounded once to `dtype`.  K must be a multiple of 64 and N of 4; x and w
- * rows 16-byte aligned, y rows and bias 8-byte aligned.
- *
- * Replaces, in the model's layer loop, `F.gelu(layer.ffn_in(ffn_input),
- * approximate="none")` (reference transformer_opt/submission.py:507; the
- * organizer's block, benchmarks/torch_transformer_benchmark.py:141), a
- * library GEMM followed by a separate GELU pass.  The reference's own fused
- * attempt is the fp32 Triton `gemm_gelu` experiment
- * (benchmarks/experiments/c15_components.py:131-166); it has no ABI to bind.
- */
-ttk_status ttk_linear_gelu_fwd(const void* x, const void* w, const void* bias,
-                               void* y, int dtype, int64_t M, int64_t N,
-                               int64_t K, int64_t ldx, int64_t ldw,
-                               int64_t ldy, void* stream);
 
 /*
  * Exact (erf) GELU, elementwise: y[i] = x[i] * Phi(x[i]) for i < n, computed

@@ -150,24 +150,6 @@ def test_missing_library_fails_loudly_in_a_fresh_process(tmp_path):
     assert "FWD True" in out.stdout, out.stderr
 
 
-def test_linear_gelu_argument_errors_are_reported_without_launching():
-    lib = _native.load()
-    f = lib.ttk_linear_gelu_fwd
-    # (x, w, bias, y, dtype, M, N, K, ldx, ldw, ldy, stream)
-    assert f(16, 16, None, 16, _native.TTK_F32, 4, 8, 64, 64, 64, 8, None) == _native.TTK_EUNSUPPORTED
-    assert "bf16 or fp16" in _native.last_error()
-    assert f(16, 16, None, 16, _native.TTK_BF16, 4, 8, 48, 48, 48, 8, None) == _native.TTK_EUNSUPPORTED
-    assert "multiple of 64" in _native.last_error()
-    assert f(16, 16, None, 16, _native.TTK_BF16, 4, 6, 64, 64, 64, 8, None) == _native.TTK_EUNSUPPORTED
-    assert f(16, 16, None, 16, _native.TTK_BF16, 4, 8, 64, 32, 64, 8, None) == _native.TTK_EINVAL
-    assert f(None, 16, None, 16, _native.TTK_BF16, 4, 8, 64, 64, 64, 8, None) == _native.TTK_EINVAL
-    assert f(24, 16, None, 16, _native.TTK_BF16, 4, 8, 64, 64, 64, 8, None) == _native.TTK_EUNSUPPORTED
-    assert "16-byte aligned" in _native.last_error()
-    assert f(16, 16, 12, 16, _native.TTK_BF16, 4, 8, 64, 64, 64, 8, None) == _native.TTK_EUNSUPPORTED
-    assert "8-byte aligned" in _native.last_error()
-    assert f(16, 16, None, 16, _native.TTK_BF16, 0, 8, 64, 64, 64, 8, None) == _native.TTK_OK
-
-
 def test_gelu_argument_errors_are_reported_without_launching():
     lib = _native.load()
     f = lib.ttk_gelu_fwd

@@ -336,56 +336,6 @@ extern "C" ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u, c
   return TTK_OK;
 }
 
-extern "C" ttk_status ttk_linear_gelu_fwd(const void* x, const void* w, const void* bias, void* y,
-                                          int dtype, int64_t M, int64_t N, int64_t K, int64_t ldx,
-                                          int64_t ldw, int64_t ldy, void* stream) {
-  g_error[0] = '\0';
-  if (dtype != TTK_BF16 && dtype != TTK_F16) {
-    return fail(TTK_EUNSUPPORTED, "linear_gelu: dtype code %d is not bf16 or fp16", dtype);
-  }
-  if (M < 0 || N <= 0 || K <= 0) {
-    return fail(TTK_EINVAL, "linear_gelu: M must be >= 0 and N, K > 0 (M=%lld N=%lld K=%lld)",
-                (long long)M, (long long)N, (long long)K);
-  }
-  if (K % 64 != 0 || N % 4 != 0) {
-    return fail(TTK_EUNSUPPORTED, "linear_gelu: K=%lld must be a multiple of 64 and N=%lld of 4",
-                (long long)K, (long long)N);
-  }
-  if (ldx < K || ldw < K || ldy < N) {
-    return fail(TTK_EINVAL, "linear_gelu: row strides must cover the rows (ldx=%lld ldw=%lld ldy=%lld)",
-                (long long)ldx, (long long)ldw, (long long)ldy);
-  }
-  if (M == 0) return TTK_OK;
-  if (!x || !w || !y) return fail(TTK_EINVAL, "linear_gelu: x, w and y must not be NULL");
-  if (!aligned16(x) || !aligned16(w) || ldx % 8 != 0 || ldw % 8 != 0) {
-    return fail(TTK_EUNSUPPORTED, "linear_gelu: x and w rows must be 16-byte aligned");
-  }
-  if ((reinterpret_cast<uintptr_t>(y) & 7u) != 0 || ldy % 4 != 0 ||
-      (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 7u) != 0)) {
-    return fail(TTK_EUNSUPPORTED, "linear_gelu: y rows and bias must be 8-byte aligned");
-  }
-  // Element offsets of x and w rows are kept in 32-bit integers.
-  if (M * ldx > kIntMax || N * ldw > kIntMax || M > kIntMax || N > kIntMax) {
-    return fail(TTK_EUNSUPPORTED, "linear_gelu: operands exceed 2^31 elements");
-  }
-  ttk::LinearParams p{};
-  p.x = x;
-  p.w = w;
-  p.bias = bias;
-  p.y = y;
-  p.M = static_cast<int>(M);
-  p.N = static_cast<int>(N);
-  p.K = static_cast<int>(K);
-  p.ldx = static_cast<int>(ldx);
-  p.ldw = static_cast<int>(ldw);
-  p.ldy = static_cast<int>(ldy);
-  const hipError_t err = ttk::launch_linear_gelu(dtype, p, static_cast<hipStream_t>(stream));
-  if (err != hipSuccess) {
-    return fail(TTK_ELAUNCH, "linear_gelu: launch failed: %s", hipGetErrorString(err));
-  }
-  return TTK_OK;
-}
-
 extern "C" ttk_status ttk_gelu_fwd(const void* x, void* y, int dtype, int64_t n, void* stream) {
   g_error[0] = '\0';
   const int es = elem_bytes(dtype);

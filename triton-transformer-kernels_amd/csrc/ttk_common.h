@@ -128,17 +128,6 @@ struct LnParams {
   int zero_norm;
 };
 
-// Launch parameters of the fused Linear + GELU kernel (element row strides).
-struct LinearParams {
-  const void* x;     // [M, K], row stride ldx
-  const void* w;     // [N, K], row stride ldw
-  const void* bias;  // [N] or nullptr
-  void* y;           // [M, N], row stride ldy
-  int M, N, K;
-  int ldx, ldw, ldy;
-  int tiles_m;       // set by the launcher
-};
-
 // Host-side launchers (defined next to their kernels).  Return a HIP error.
 // launch_attention fills p.pair / p.units / the split plan and sizes the
 // grid itself.  `workspace` (workspace_bytes, 256-byte aligned) may be null;
@@ -153,8 +142,6 @@ int64_t attention_workspace_bytes(int dtype, int D, bool causal, int64_t BH, int
 
 hipError_t launch_residual_layernorm(int dtype, const LnParams& p, bool vector_path,
                                      int vectors_per_lane, hipStream_t stream);
-
-hipError_t launch_linear_gelu(int dtype, LinearParams& p, hipStream_t stream);
 
 // Exact GELU over n contiguous elements of dtype (0 fp32, 1 bf16, 2 fp16).
 hipError_t launch_gelu(int dtype, const void* x, void* y, int64_t n, hipStream_t stream);

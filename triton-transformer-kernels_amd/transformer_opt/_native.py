@@ -34,10 +34,9 @@ EXPORTED_SYMBOLS = (
     "ttk_attention_fwd_ws",
     "ttk_attention_fwd_noalloc",
     "ttk_residual_layernorm_fwd",
-    "ttk_linear_gelu_fwd",
     "ttk_gelu_fwd",
 )
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -80,10 +79,6 @@ def _configure(lib: ctypes.CDLL) -> None:
     lib.ttk_residual_layernorm_fwd.argtypes = [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int,
         _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int, _vp,
-    ]
-    lib.ttk_linear_gelu_fwd.restype = ctypes.c_int
-    lib.ttk_linear_gelu_fwd.argtypes = [
-        _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
     ]
     lib.ttk_gelu_fwd.restype = ctypes.c_int
     lib.ttk_gelu_fwd.argtypes = [_vp, _vp, ctypes.c_int, _i64, _vp]

@@ -2,7 +2,6 @@
 
 from .attention import hip_attention, hip_available, triton_attention, triton_available
 from .gelu import gelu, gelu_
-from .linear import linear_gelu, linear_gelu_supported
 from .residual_layer_norm import fused_residual_layer_norm, layer_norm, short_layer_norm
 
 __all__ = [
@@ -12,8 +11,6 @@ __all__ = [
     "hip_attention",
     "hip_available",
     "layer_norm",
-    "linear_gelu",
-    "linear_gelu_supported",
     "short_layer_norm",
     "triton_attention",
     "triton_available",
