@@ -42,12 +42,10 @@ __device__ __forceinline__ float to_f32(F16, unsigned short v) {
 }
 
 __device__ __forceinline__ float from_f32(F32, float v) { return v; }
-// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN), the rounding torch uses.
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN), the rounding torch uses:
+// the gfx950 conversion instruction (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ unsigned short from_f32(BF16, float v) {
-  unsigned int u = __float_as_uint(v);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<unsigned short>(u >> 16);
+  return __builtin_bit_cast(unsigned short, static_cast<__bf16>(v));
 }
 __device__ __forceinline__ unsigned short from_f32(F16, float v) {
   _Float16 h = static_cast<_Float16>(v);  // v_cvt_f16_f32: round to nearest even
