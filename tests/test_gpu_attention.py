@@ -635,6 +635,42 @@ def test_short_sequence_persistent_grid(gpu_ready, batch, seq_len, heads, head_d
         assert bool((actual[1] == 0).all())
 
 
+def _short_case(rng: torch.Generator):
+    """One randomized fp32 non-causal case with S <= 64 (the short-sequence kernel)."""
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731
+    batch = int(torch.randint(1, 41, (1,), generator=rng))
+    seq_len = int(torch.randint(1, 65, (1,), generator=rng))
+    heads = int(torch.randint(1, 41, (1,), generator=rng))
+    head_dim = pick([32, 64])
+    mask_mode = pick(["none", "none", "prefix", "holes"])
+    layout = pick(["contiguous", "bhsd", "packed"])
+    scale = pick([None, None, 0.05, 0.3])
+    return batch, seq_len, heads, head_dim, mask_mode, layout, scale
+
+
+@pytest.mark.parametrize("case_seed", range(48))
+def test_randomized_short_sequences(gpu_ready, case_seed):
+    # Seeded random sweep of the short-sequence kernel's envelope: B and H up
+    # to 40 (up to 3200 items, so some wavefronts walk two), S from 1 to 64
+    # (one or two 32-query halves, ragged key ends), head dims 32 and 64,
+    # every layout, prefix and holed masks, default and explicit scales.
+    rng = torch.Generator().manual_seed(7000 + case_seed)
+    batch, seq_len, heads, head_dim, mask_mode, layout, scale = _short_case(rng)
+    q, k, v = _layout_inputs((batch, seq_len, heads, head_dim), layout, rng)
+    if mask_mode == "holes":
+        mask = torch.rand(batch, seq_len, generator=rng) > 0.35
+    else:
+        mask = make_mask(mask_mode, batch, seq_len)
+    actual = run_hip(q, k, v, mask, False, scale=scale)
+    reference = oracle(q.cpu(), k.cpu(), v.cpu(), mask, False, scale=scale)
+    label = f"case {case_seed}: {(batch, seq_len, heads, head_dim)} mask={mask_mode} layout={layout} scale={scale}"
+    assert contract_failures(actual, reference) == 0, label
+    tight_check(actual, reference, torch.float32)
+    if mask is not None:
+        empty = ~mask.any(dim=1)
+        assert bool((actual[empty] == 0).all()), label
+
+
 def test_twin_grid_config5b_shape_with_padding(gpu_ready):
     # Config 5b's attention (fp32, B=512, S=64, H=8, D=64, non-causal) with
     # right padding of every length 1..64 and random holes, every head
