@@ -280,9 +280,15 @@ __device__ __forceinline__ void apply_mask(f32x16 (&s)[NSB], int k0, uint64_t kv
 // Waves per SIMD the register budget is sized for: two workgroups per CU,
 // except fp32 head_dim 128, whose live state (64 accumulator + 64 Q registers
 // + score tiles + staging) does not fit 256 registers; it runs one workgroup
-// per CU with the accumulators in AGPRs.
+// per CU with the accumulators in AGPRs; and 16-bit head_dim <= 64, sized for
+// three (at most 168 VGPRs; the LDS of three workgroups fits).  The 16-bit
+// loop is VALU-issue and latency bound, so the third workgroup pays: left to
+// itself the compiler gave the causal head_dim-64 kernel 176 VGPRs (two
+// workgroups per CU), and capping it at 168 - five registers spilled, reloaded
+// only on the accumulator-rescale path - made config 4's attention 5-7 %
+// faster.
 template <bool F32, int D>
-constexpr int kMinWaves = (D >= 128 && F32) ? 1 : 2;
+constexpr int kMinWaves = (D >= 128 && F32) ? 1 : ((!F32 && D <= 64) ? 3 : 2);
 
 // ----------------------------------------------------------------------------
 // fp32
