@@ -1509,7 +1509,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     //   phase B: O^T += V(t)^T.P(t), interleaved with the row max of S(t+1);
     //            then the row sum of P(t) and the reference decision for
     //            tile t+1 (with the accumulator rescale when it moves).
-    auto phase_a = [&](int kbuf, f32x16 (&sn)[NSB], const f32x16 (&s)[NSB], float mc)
+    auto phase_a = [&](int kbuf, f32x16 (&sn)[NSB], const f32x16 (&s)[NSB], float mc, auto&& hook)
         __attribute__((always_inline)) {
       constexpr int NQK = G * NSB;  // Q.K MFMAs of a tile
       constexpr int E = NSB * 16;   // score elements per lane
@@ -1538,12 +1538,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
 #pragma unroll
           for (int sb = 0; sb < NSB; ++sb) kr[g % PDK][sb] = kread(kbuf, sb, g + PDK);
         }
+        hook(g);
         fence();
       }
     };
     // ADD_SUM: whether P(t) still has to enter the row sum (the generic
     // softmax counts its P when producing it).
-    auto phase_b = [&](auto add_sum_tag, int vbuf, const f32x16 (&sn)[NSB])
+    auto phase_b = [&](auto add_sum_tag, int vbuf, const f32x16 (&sn)[NSB], auto&& hook)
         __attribute__((always_inline)) {
       constexpr bool ADD_SUM = decltype(add_sum_tag)::value;
       constexpr int E = NSB * 16;
@@ -1562,6 +1563,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
           const int e = PER * idx + j;
           mt = fmaxf(mt, sn[e >> 4][e & 15]);
         }
+        hook(idx);
         fence();
       }
       if constexpr (ADD_SUM) l_run += sum_packed<T>(pk);
@@ -1667,20 +1669,32 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       }
       dma_v_full(t1 & 1, t1);
       qk(std::false_type{}, t1 & 1, NSB, sa);
-      phase_b(std::false_type{}, kt0 & 1, sa);
+      phase_b(std::false_type{}, kt0 & 1, sa, [](int) {});
       finish_tile(t1);
       // Tile t + 1 for t = t1 .. n_full - 2.
       auto steady = [&](int t, const f32x16 (&cur)[NSB], f32x16 (&nxt)[NSB])
           __attribute__((always_inline)) {
         const int kb = t & 1;
-        if (t + 2 < n_full) {
-          dma_k_full(kb, t + 2);
-        } else if (t + 2 < kt1) {
-          dma_k(kb, t + 2);
-        }
-        dma_v_full(kb ^ 1, t + 1);
-        phase_a(kb ^ 1, nxt, cur, ref_exp());
-        phase_b(std::true_type{}, kb, nxt);
+        // The copies of K(t+2) and V(t+1) are spread over the MFMA groups of
+        // both phases instead of issued back to back at the top of the tile.
+        static_assert(KPW <= G && 2 * VPW - 1 <= NSTEP, "a copy slot for every copy");
+        const bool kfull = t + 2 < n_full;
+        if (!kfull && t + 2 < kt1) dma_k(kb, t + 2);
+        const St* kt = K + static_cast<int64_t>(t + 2) * BN * p.ks;
+        const St* vt = V + static_cast<int64_t>(t + 1) * BN * p.vs;
+        phase_a(kb ^ 1, nxt, cur, ref_exp(), [&](int g) __attribute__((always_inline)) {
+          if (g < KPW) {
+            const int j = wave + NW * g;
+            if (kfull && j < NK) dma16(kt, koff[g], &smK[kb][512 * j]);
+          }
+        });
+        phase_b(std::true_type{}, kb, nxt, [&](int idx) __attribute__((always_inline)) {
+          if (idx % 2 == 0 && idx / 2 < VPW) {
+            const int i = idx / 2;
+            const int j = wave + NW * i;
+            if (j < NV) dma16(vt, voff[i], &smV[kb ^ 1][512 * j]);
+          }
+        });
         finish_tile(t + 1);
       };
       int t = t1;
