@@ -21,21 +21,25 @@
 //       lane halves 0 and 1.  No transpose, no LDS round trip for P.
 // * K and V tiles are double-buffered in LDS with one barrier per tile.  K
 //   rows are padded by 16 bytes, so the 16-byte MFMA operand reads of 16
-//   consecutive key rows start 4 banks apart and cover all 64 banks, and
+//   consecutive key rows start on distinct banks and cover all 64 banks, and
 //   every per-step operand address is the lane's base plus an immediate.
 //     - fp32: the next tile's global loads are issued into registers before
 //       the current tile's MFMAs and written to the other buffer after them.
 //       The fp32 MFMA is 16 passes long, so the matrix core is the bound and
 //       the softmax VALU of one wavefront runs under the MFMAs of the other
 //       wavefront on the SIMD.
-//     - bf16/fp16: the 8-pass MFMA leaves the softmax as the bound (per tile
-//       a wavefront issues 32 MFMAs against ~110 VALU instructions and 32
-//       v_exp_f32), so the loop is
-//       software-pipelined: iteration t computes S(t) = K(t).Q^T and then one
-//       instruction stream interleaving the P.V MFMAs of tile t-1 with the
-//       softmax of tile t.  K(t+1) and V(t) are copied global->LDS by LDS-DMA
-//       (global_load_lds_dwordx4, no register staging); V stays row-major and
-//       the P.V operand is read with the transposing ds_read_b64_tr_b16.
+//     - bf16/fp16: the 8-pass MFMA leaves the softmax as the bound (per
+//       64-key tile a wavefront issues 16 (head_dim 64) or 32 (128) MFMAs
+//       against ~140 VALU instructions, 32 of them v_exp_f32), so the loop
+//       is software-pipelined.  Unmasked tiles run two phases per tile:
+//       Q.K of tile t+1 interleaved with the exp2 and 16-bit rounding of
+//       tile t's scores, then the P.V of tile t interleaved with the row max
+//       of tile t+1.  Key-masked launches run one stream interleaving the
+//       P.V of tile t-1 with the softmax of tile t.  K and V tiles are
+//       copied global->LDS by LDS-DMA (global_load_lds_dwordx4, no register
+//       staging), spread over the MFMA groups of the pipelined loop; V stays
+//       row-major and the P.V operand is read with the transposing
+//       ds_read_b64_tr_b16.
 // * Masking: key validity (key mask and key < S) is a wave-uniform 64-bit
 //   ballot per tile; with the lane's causal limit it becomes one bit mask per
 //   32-key sub-block.  Only tiles that need it (diagonal, ragged end, key
