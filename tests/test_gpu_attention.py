@@ -216,6 +216,27 @@ def test_running_max_growth_across_tiles(gpu_ready, dtype, head_dim, ramp, causa
     tight_check(actual, reference, dtype, tol=1e-4)
 
 
+@pytest.mark.parametrize("seq_len", [192, 193, 255, 256, 257, 320, 383, 448])
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_pipelined_loop_copy_boundaries(gpu_ready, seq_len, head_dim, dtype, causal):
+    # Unmasked 16-bit launches run full key tiles through the two-phase loop,
+    # whose K(t+2) / V(t+1) copies are issued between its MFMA groups; where
+    # K(t+2) is the ragged last tile or past the query tile's last key tile
+    # the copy takes the generic path instead.  These lengths put the loop's
+    # end on each side of those cases, for every wavefront of a query tile.
+    g = torch.Generator().manual_seed(seq_len * 7 + head_dim)
+    shape = (2, seq_len, 3, head_dim)
+    q = torch.randn(shape, generator=g).to(dtype)
+    k = torch.randn(shape, generator=g).to(dtype)
+    v = torch.randn(shape, generator=g).to(dtype)
+    actual = run_hip(q, k, v, None, causal)
+    reference = oracle(q, k, v, None, causal)
+    assert contract_failures(actual, reference) == 0
+    tight_check(actual, reference, dtype)
+
+
 def test_all_keys_masked_is_finite_zero(gpu_ready):
     # Reference tests/test_gpu_attention.py:114-128.
     g = torch.Generator().manual_seed(3)
