@@ -217,7 +217,7 @@ def test_running_max_growth_across_tiles(gpu_ready, dtype, head_dim, ramp, causa
 
 
 @pytest.mark.parametrize("seq_len", [192, 193, 255, 256, 257, 320, 383, 448])
-@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("head_dim", [8, 16, 32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("causal", [True, False])
 def test_pipelined_loop_copy_boundaries(gpu_ready, seq_len, head_dim, dtype, causal):
