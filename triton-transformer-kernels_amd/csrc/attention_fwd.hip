@@ -1128,10 +1128,15 @@ struct H16Cfg {
   static constexpr int KS = DK + 8;                  // LDS K row stride (elements, 16-byte pad)
   static constexpr int NDB = (D + 31) / 32;          // output blocks of 32 d-rows
   static constexpr int G = DK / 16;                  // Q.K k-steps of 16
-  // LDS V row stride (elements): row-major V tile whose stride is 16 dwords
-  // mod 64 banks, so the 4 key rows one half-wave reads with the transposing
-  // load fall on disjoint banks.
-  static constexpr int VS = D == 128 ? 160 : D == 64 ? 96 : D;
+  // LDS V row stride (elements) of the row-major V tile.  The 4 key rows one
+  // half-wave reads with the transposing load must fall on disjoint banks:
+  // head_dim 128 pads its rows to a stride of 16 dwords mod 64 banks; head_dim
+  // 64 keeps them unpadded (128 bytes, so rows r and r + 2 share banks) and
+  // instead swaps the two 32-column halves of the rows with bit 1 set (VSWZ:
+  // the slot of 16-byte chunk c in row r is c ^ 4*((r >> 1) & 1)), which
+  // copies 8 chunks per row instead of 12.
+  static constexpr bool VSWZ = D == 64;
+  static constexpr int VS = D == 128 ? 160 : D;
   static constexpr int VCH = VS / 8;                 // 16-byte chunks per LDS V row
   // Head dims below 32 read up to d = 31 with the transposing load (rows
   // d >= D of the result are never stored); the slack keeps those reads of
@@ -1211,6 +1216,8 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
   }
   // V: LDS-DMA into row-major rows of VCH 16-byte chunks (read back with the
   // transposing load); pad chunks copy a data chunk of the same row again.
+  // With VSWZ the lane filling slot (row, cc) copies chunk cc ^ vswz(row).
+  auto vswz = [](int row) { return C::VSWZ ? 4 * ((row >> 1) & 1) : 0; };
   constexpr int NV = (BN * VCH + 63) / 64;
   constexpr int VPW = (NV + NW - 1) / NW;
   unsigned voff[VPW];
@@ -1219,13 +1226,16 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     const int pos = 64 * (wave + NW * i) + lane;
     const int row = pos / VCH;
     const int cc = pos - row * VCH;
-    voff[i] = 2u * static_cast<unsigned>(row * static_cast<int>(p.vs) + 8 * (cc < CPR ? cc : cc - CPR));
+    voff[i] = 2u * static_cast<unsigned>(row * static_cast<int>(p.vs) + 8 * ((cc < CPR ? cc : cc - CPR) ^ vswz(row)));
   }
   // Per-lane base of the transposing V reads: lane i of 16-lane group g
   // addresses key row 4*(g/2) + i/4 and d = 16*(g%2) + 4*(i%4), so lane
   // (m, h) receives V[4h + 0..3][m] (see lds_read_tr16); P.V step (kstep,
   // db) adds 16*kstep rows and 32*db columns, its upper four keys 8 rows.
+  // With VSWZ the rows a lane reads all have bit 1 equal to lane bit 3, so
+  // the swap of 32-column halves is one per-lane flip of the db offset.
   const int vbase = (4 * h + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int vflip = C::VSWZ ? 32 * ((lane >> 3) & 1) : 0;
 
   {
     // 16-bit workgroups run one query tile (never paired: a second pass costs
@@ -1299,7 +1309,8 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
             const int row = pos / VCH;
             const int cc = pos - row * VCH;
             const int rrel = min(t * BN + row, S - 1) - t * BN;
-            dma16(vt, 2u * static_cast<unsigned>(rrel * static_cast<int>(p.vs) + 8 * (cc < CPR ? cc : cc - CPR)),
+            dma16(vt, 2u * static_cast<unsigned>(rrel * static_cast<int>(p.vs) +
+                                                 8 * ((cc < CPR ? cc : cc - CPR) ^ vswz(row))),
                   &smV[buf][512 * j]);
           }
         }
@@ -1343,7 +1354,8 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     auto vread = [&](int buf, int idx) __attribute__((always_inline)) -> u16x8 {
       const int db = idx % NDB;
       const int kstep = idx / NDB;  // sb * 2 + j
-      const unsigned short* base = &smV[buf][vbase + 16 * kstep * VS + 32 * db];
+      const int col = C::VSWZ ? vbase + ((32 * db) ^ vflip) : vbase + 32 * db;
+      const unsigned short* base = &smV[buf][col + 16 * kstep * VS];
       const u16x4 lo = lds_read_tr16(base);
       const u16x4 hi = lds_read_tr16(base + 8 * VS);
       return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
