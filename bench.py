@@ -307,8 +307,10 @@ def cpu_baseline(time_budget_s: float = 8.0):
     }
 
 
-def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidden: int = 4096) -> int:
-    """Launch one kernel `steps` times (after `warmup`) for a profiler run.
+def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidden: int = 4096,
+                 settle_s: float = 0.0) -> int:
+    """Launch one kernel `steps` times (after `settle_s` seconds of untimed launches
+    and `warmup` more) for a profiler run.
 
     attention:      fp32 causal [8,S,16,64], S = --seq-len (1024: the headline step)
     attention_bf16: bf16 causal [1,16384,32,128] (config 5a)
@@ -411,6 +413,13 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         fn = lambda: dst.copy_(src)  # noqa: E731
         work = 2.0 * src.numel() * 4
     with torch.inference_mode():
+        # The same clock settling as the headline run, so a profile of the
+        # step sees the clocks the bench line is measured at.
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < settle_s:
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -481,7 +490,7 @@ def main() -> int:
     dev_name = torch.cuda.get_device_name(0)
     log(f"device {dev_name}; library {_native.library_path()}")
     if args.profile_only:
-        return profile_only(args.profile_only, args.steps, args.warmup, args.seq_len, args.hidden)
+        return profile_only(args.profile_only, args.steps, args.warmup, args.seq_len, args.hidden, args.settle_s)
 
     # ---- headline: config 2, fp32 causal attention, S=1024 -----------------
     B, S, H, D = 8, 1024, 16, 64
