@@ -1129,14 +1129,15 @@ struct H16Cfg {
   static constexpr int NDB = (D + 31) / 32;          // output blocks of 32 d-rows
   static constexpr int G = DK / 16;                  // Q.K k-steps of 16
   // LDS V row stride (elements) of the row-major V tile.  The 4 key rows one
-  // half-wave reads with the transposing load must fall on disjoint banks:
-  // head_dim 128 pads its rows to a stride of 16 dwords mod 64 banks; head_dim
-  // 64 keeps them unpadded (128 bytes, so rows r and r + 2 share banks) and
-  // instead swaps the two 32-column halves of the rows with bit 1 set (VSWZ:
-  // the slot of 16-byte chunk c in row r is c ^ 4*((r >> 1) & 1)), which
-  // copies 8 chunks per row instead of 12.
-  static constexpr bool VSWZ = D == 64;
-  static constexpr int VS = D == 128 ? 160 : D;
+  // half-wave reads with the transposing load must fall on disjoint banks.
+  // Rows stay unpadded and, for head_dim 64 and 128 (VSWZ), 32-column blocks
+  // are permuted per row instead: 16-byte chunk c of row r sits in slot
+  // c ^ 4*((r >> 1) & 1) (head_dim 64: 128-byte rows, rows r and r + 2 share
+  // banks) or c ^ 4*(r & 3) (head_dim 128: 256-byte rows, every row starts on
+  // bank 0).  That copies 8 / 16 chunks per row instead of the 12 / 20 of a
+  // padded stride.
+  static constexpr bool VSWZ = D == 64 || D == 128;
+  static constexpr int VS = D;
   static constexpr int VCH = VS / 8;                 // 16-byte chunks per LDS V row
   // Head dims below 32 read up to d = 31 with the transposing load (rows
   // d >= D of the result are never stored); the slack keeps those reads of
@@ -1217,7 +1218,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
   // V: LDS-DMA into row-major rows of VCH 16-byte chunks (read back with the
   // transposing load); pad chunks copy a data chunk of the same row again.
   // With VSWZ the lane filling slot (row, cc) copies chunk cc ^ vswz(row).
-  auto vswz = [](int row) { return C::VSWZ ? 4 * ((row >> 1) & 1) : 0; };
+  auto vswz = [](int row) { return C::VSWZ ? (D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1)) : 0; };
   constexpr int NV = (BN * VCH + 63) / 64;
   constexpr int VPW = (NV + NW - 1) / NW;
   unsigned voff[VPW];
@@ -1232,10 +1233,11 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
   // addresses key row 4*(g/2) + i/4 and d = 16*(g%2) + 4*(i%4), so lane
   // (m, h) receives V[4h + 0..3][m] (see lds_read_tr16); P.V step (kstep,
   // db) adds 16*kstep rows and 32*db columns, its upper four keys 8 rows.
-  // With VSWZ the rows a lane reads all have bit 1 equal to lane bit 3, so
-  // the swap of 32-column halves is one per-lane flip of the db offset.
+  // With VSWZ the rows a lane reads all share their low two bits with lane
+  // bits 2-3 (16*kstep and 8 rows leave them alone), so the block permutation
+  // is one per-lane XOR of the db offset.
   const int vbase = (4 * h + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const int vflip = C::VSWZ ? 32 * ((lane >> 3) & 1) : 0;
+  const int vflip = C::VSWZ ? (D == 128 ? 32 * ((lane >> 2) & 3) : 32 * ((lane >> 3) & 1)) : 0;
 
   {
     // 16-bit workgroups run one query tile (never paired: a second pass costs
