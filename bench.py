@@ -25,8 +25,11 @@ Also reported in the same line:
 * ``secondary``: the S sweep {256..4096} causal/non-causal (config 2), the
   residual+LayerNorm HBM GB/s per hidden size with rotating input sets larger
   than the 256 MB MALL (config 3), bf16 long-sequence attention (config 5a)
-  and encoder tokens/s with hipGraph replay (config 4, fp32 and bf16).
-  ``--quick`` skips the secondary block.
+  and encoder tokens/s with hipGraph replay (config 4, fp32 and bf16).  Each
+  figure there follows 1 s of untimed calls of its own workload (the clock
+  follows the power draw of the work in flight), and each kernel figure is
+  the average launch over back-to-back launches between two events, as for
+  ``roofline``.  ``--quick`` skips the secondary block.
 
 One GPU only: ``--gpus`` other than 1 exits with a message.
 """
@@ -97,6 +100,47 @@ def make_qkv(batch, seq_len, heads, head_dim, dtype, seed):
                  for _ in range(3))
 
 
+# Seconds of untimed calls of a secondary workload before its warm-up: the
+# GPU's clock follows the power draw of the work in flight with a lag of
+# tens of milliseconds or more, so a short measurement taken right after a
+# different workload (or idling) runs at that workload's clock.
+SECONDARY_SETTLE_S = 1.0
+
+
+def settle(fn, seconds: float) -> None:
+    """Call `fn` for about `seconds` of wall time (synchronising every 10 calls)."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def back_to_back_ms(fn, steps: int, warmup: int, settle_s: float = SECONDARY_SETTLE_S) -> float:
+    """Average time per call (ms) of `steps` back-to-back calls between two
+    events on the current stream, after `settle_s` seconds and `warmup` more
+    untimed calls: the launch duration rocprofv3 --stats averages (an event
+    pair around every launch adds microseconds of its own to a ~50 us
+    kernel)."""
+    import torch
+
+    settle(fn, settle_s)
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    begin = torch.cuda.Event(enable_timing=True)
+    finish = torch.cuda.Event(enable_timing=True)
+    begin.record(stream)
+    for _ in range(steps):
+        fn()
+    finish.record(stream)
+    torch.cuda.synchronize()
+    return begin.elapsed_time(finish) / steps
+
+
 def attention_tflops(batch, seq_len, heads, head_dim, causal, dtype, steps=10, warmup=3):
     from transformer_opt.kernels import hip_attention
 
@@ -106,9 +150,8 @@ def attention_tflops(batch, seq_len, heads, head_dim, causal, dtype, steps=10, w
     def run():
         hip_attention(q, k, v, causal=causal, out=out)
 
-    _, ms = time_launches(run, steps, warmup)
-    med = statistics.median(ms)
-    return attention_flops(batch, heads, seq_len, head_dim, causal) / (med * 1e-3) / 1e12, med
+    ms = back_to_back_ms(run, steps, warmup)
+    return attention_flops(batch, heads, seq_len, head_dim, causal) / (ms * 1e-3) / 1e12, ms
 
 
 def packed_attention_5b_us(steps: int = 50, warmup: int = 5) -> float:
@@ -123,17 +166,7 @@ def packed_attention_5b_us(steps: int = 50, warmup: int = 5) -> float:
     packed = torch.randn(512, 64, 3, 8, 64, device="cuda", generator=g)
     q, k, v = packed.unbind(dim=2)
     out = torch.empty(512, 64, 8, 64, device="cuda")
-    for _ in range(warmup):
-        hip_attention(q, k, v, causal=False, out=out)
-    torch.cuda.synchronize()
-    begin = torch.cuda.Event(enable_timing=True)
-    finish = torch.cuda.Event(enable_timing=True)
-    begin.record()
-    for _ in range(steps):
-        hip_attention(q, k, v, causal=False, out=out)
-    finish.record()
-    torch.cuda.synchronize()
-    return begin.elapsed_time(finish) / steps * 1e3
+    return back_to_back_ms(lambda: hip_attention(q, k, v, causal=False, out=out), steps, warmup) * 1e3
 
 
 def layer_norm_gbps(hidden: int, rows: int = 32768, steps: int = 50, warmup: int = 5):
@@ -165,18 +198,7 @@ def layer_norm_gbps(hidden: int, rows: int = 32768, steps: int = 50, warmup: int
         fused_residual_layer_norm(x, u, w, b, 1e-5)
 
     with torch.inference_mode():
-        for _ in range(warmup):
-            run()
-        torch.cuda.synchronize()
-        stream = torch.cuda.current_stream()
-        begin = torch.cuda.Event(enable_timing=True)
-        finish = torch.cuda.Event(enable_timing=True)
-        begin.record(stream)
-        for _ in range(steps):
-            run()
-        finish.record(stream)
-        torch.cuda.synchronize()
-    ms = begin.elapsed_time(finish) / steps
+        ms = back_to_back_ms(run, steps, warmup)
     return layer_norm_bytes(rows, hidden) / (ms * 1e-3) / 1e9, ms, nsets
 
 
@@ -201,6 +223,7 @@ def model_tokens_per_second(dtype_name: str, cfg=ENCODER_CONFIG4, steps: int = 5
     g.manual_seed(1234)
     x = torch.randn(batch, seq_len, d_model, generator=g, device="cuda").to(dtype)
     with torch.inference_mode():
+        settle(lambda: model(x), SECONDARY_SETTLE_S)
         wall, ms = time_launches(lambda: model(x), steps, warmup)
         replays = model.cuda_graph_replays
     med = statistics.median(ms)
@@ -591,7 +614,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         # The attention of the config-4 bf16 encoder and of the config-5b
         # encoder (non-causal fp32 on packed-QKV views), per launch.
-        tf, ms = attention_tflops(4, 2048, 16, 64, True, torch.bfloat16, steps=20, warmup=5)
+        tf, ms = attention_tflops(4, 2048, 16, 64, True, torch.bfloat16, steps=50, warmup=20)
         secondary["attention_bf16_causal_B4_H16_S2048_D64"] = {
             "tflops": round(tf, 2), "us": round(ms * 1e3, 2),
             "frac_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
