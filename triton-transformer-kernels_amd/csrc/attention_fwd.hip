@@ -1215,9 +1215,10 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     const int cc = pos - row * KCH;
     koff[i] = 2u * static_cast<unsigned>(row * static_cast<int>(p.ks) + 8 * (cc < CPR ? cc : 0));
   }
-  // V: LDS-DMA into row-major rows of VCH 16-byte chunks (read back with the
-  // transposing load); pad chunks copy a data chunk of the same row again.
-  // With VSWZ the lane filling slot (row, cc) copies chunk cc ^ vswz(row).
+  // V: LDS-DMA into unpadded row-major rows of VCH 16-byte chunks (read back
+  // with the transposing load); with VSWZ the lane filling slot (row, cc)
+  // copies chunk cc ^ vswz(row).
+  static_assert(VCH == CPR, "V rows are unpadded");
   auto vswz = [](int row) { return C::VSWZ ? (D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1)) : 0; };
   constexpr int NV = (BN * VCH + 63) / 64;
   constexpr int VPW = (NV + NW - 1) / NW;
@@ -1227,7 +1228,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     const int pos = 64 * (wave + NW * i) + lane;
     const int row = pos / VCH;
     const int cc = pos - row * VCH;
-    voff[i] = 2u * static_cast<unsigned>(row * static_cast<int>(p.vs) + 8 * ((cc < CPR ? cc : cc - CPR) ^ vswz(row)));
+    voff[i] = 2u * static_cast<unsigned>(row * static_cast<int>(p.vs) + 8 * (cc ^ vswz(row)));
   }
   // Per-lane base of the transposing V reads: lane i of 16-lane group g
   // addresses key row 4*(g/2) + i/4 and d = 16*(g%2) + 4*(i%4), so lane
@@ -1311,8 +1312,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
             const int row = pos / VCH;
             const int cc = pos - row * VCH;
             const int rrel = min(t * BN + row, S - 1) - t * BN;
-            dma16(vt, 2u * static_cast<unsigned>(rrel * static_cast<int>(p.vs) +
-                                                 8 * ((cc < CPR ? cc : cc - CPR) ^ vswz(row))),
+            dma16(vt, 2u * static_cast<unsigned>(rrel * static_cast<int>(p.vs) + 8 * (cc ^ vswz(row))),
                   &smV[buf][512 * j]);
           }
         }
