@@ -110,11 +110,12 @@ __device__ __forceinline__ unsigned short to_bits(F16, float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Sum of the 16-bit probabilities a lane holds for one tile (NP packed u16x8
-// registers of 8 values), accumulated in fp32 with v_dot2c_f32_{bf16,f16}
-// against (1, 1): one instruction per two values, four independent chains.
-// Summing the rounded P that the P.V product uses makes the weights applied
-// to V sum to one exactly in the final division.
+// Adds the 16-bit probabilities a lane holds for one tile (NP packed u16x8
+// registers of 8 values) to the fp32 row sum acc with v_dot2c_f32_{bf16,f16}
+// against (1, 1): one instruction per two values, accumulated straight into
+// the running sum (no per-tile partial sums to clear and combine).  Summing
+// the rounded P that the P.V product uses makes the weights applied to V sum
+// to one exactly in the final division.
 __device__ __forceinline__ float dot2_ones(BF16, unsigned pair, float acc) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
@@ -126,15 +127,14 @@ __device__ __forceinline__ float dot2_ones(F16, unsigned pair, float acc) {
                                 acc, false);
 }
 template <typename T, int NP>
-__device__ __forceinline__ float sum_packed(const u16x8 (&pn)[NP]) {
-  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+__device__ __forceinline__ float add_packed(const u16x8 (&pn)[NP], float acc) {
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const u32x4 w = __builtin_bit_cast(u32x4, pn[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) part[j] = dot2_ones(T{}, w[j], part[j]);
+    for (int j = 0; j < 4; ++j) acc = dot2_ones(T{}, w[j], acc);
   }
-  return (part[0] + part[1]) + (part[2] + part[3]);
+  return acc;
 }
 
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
@@ -142,10 +142,14 @@ __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
 // Max / sum of a value and the same value in lane ^ 32 (v_permlane32_swap:
 // exchanges the upper half of the first operand with the lower half of the
 // second, so the two results hold {x[l], x[l ^ 32]} in every lane).
+// The maximum is one v_max_f32: fmaxf on the swapped words (integers to the
+// compiler) would first quiet each of them with a v_max_f32 of its own.
 __device__ __forceinline__ float max_with_other_half(float x) {
   const unsigned u = __float_as_uint(x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(r[0]), "v"(r[1]));
+  return m;
 }
 __device__ __forceinline__ float sum_with_other_half(float x) {
   const unsigned u = __float_as_uint(x);
@@ -1192,6 +1196,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
   // so 2^-100 stands in.  Masked scores stay -inf, and every allowed score
   // (|s| < 2^75) gives an exp2 argument below 2^-25, so P = 1 exactly.
   if (c == 0.0f) c = 0x1p-100f;
+  // The reference max moves once a row's max passes it by more than 8 / c
+  // (8 in log2 units, so P <= 2^8).
+  float lag = 8.0f / c;
+  // Both are wave-uniform: kept in SGPRs (a VOP3 instruction reads one SGPR
+  // operand), they leave two more VGPRs to the loop.
+  c = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(c)));
+  lag = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(lag)));
   const unsigned short sign = negate ? 0x8000u : 0u;
 
   // K: LDS-DMA into padded rows of KCH 16-byte chunks; DMA instruction j
@@ -1364,6 +1375,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     };
 
     float m_run = -INFINITY;  // running max of RAW scores
+    float m_exp = -INFINITY;  // ceil(m_run * c), kept with m_run
     float l_run = 0.0f;
     f32x16 acc[NDB];
 #pragma unroll
@@ -1432,16 +1444,18 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
     // is an exact power of two.  Call after the P.V MFMAs that use the
     // previous reference have been issued.
     auto rebase = [&](float mt) __attribute__((always_inline)) {
-      const bool need = (mt - m_run) * c > 8.0f;  // false for two -inf
+      const bool need = mt - m_run > lag;  // false for two -inf
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
         const float m_new = need ? mt : m_run;
         // 1 where the reference stays (also at -inf, where the difference
         // would be NaN), 0 from -inf, else 2^-k.
-        const float alpha = m_new == m_run ? 1.0f : fast_exp2(ceilf(m_run * c) - ceilf(m_new * c));
+        const float e_new = ceilf(m_new * c);
+        const float alpha = m_new == m_run ? 1.0f : fast_exp2(m_exp - e_new);
         l_run *= alpha;
 #pragma unroll
         for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
         m_run = m_new;
+        m_exp = e_new;
       }
     };
     auto softmax = [&](auto masked_tag, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) {
@@ -1461,7 +1475,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
           const float pr = fast_exp2(__builtin_fmaf(s[sb][r], c, -mc));
           pn[sb * 2 + (r >> 3)][r & 7] = to_bits(T{}, pr);
         }
-      l_run += sum_packed<T>(pn);
+      l_run = add_packed<T>(pn, l_run);
     };
 
     // P.V of the pending tile interleaved with the softmax of s: the first
@@ -1491,13 +1505,13 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
             mt = max_with_other_half(mt);
             // The reference for this tile: rebased now only if some row needs
             // it (the accumulator rescale waits for the last P.V step).
-            const bool need = (mt - m_run) * c > 8.0f;
+            const bool need = mt - m_run > lag;
             rebase_any = __builtin_amdgcn_ballot_w64(need) != 0;
             m_use = rebase_any && need ? mt : m_run;
             // 1 where the reference stays: a row still at -inf (no allowed
             // key so far) must not turn its zeros into NaN when another row
             // of the wavefront moves.
-            alpha = m_use == m_run ? 1.0f : fast_exp2(ceilf(m_run * c) - ceilf(m_use * c));
+            alpha = m_use == m_run ? 1.0f : fast_exp2(m_exp - ceilf(m_use * c));
             mc = ceilf((m_use == -INFINITY ? 0.0f : m_use) * c);
           }
         } else {
@@ -1515,8 +1529,9 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
 #pragma unroll
         for (int i = 0; i < NDB; ++i) acc[i] *= alpha;
         m_run = m_use;
+        m_exp = ceilf(m_use * c);
       }
-      l_run += sum_packed<T>(pn);
+      l_run = add_packed<T>(pn, l_run);
     };
     // Pipelined full tiles (launches without a key mask).  Q.K runs one tile
     // ahead, so each wavefront has matrix-core work beside its softmax VALU
@@ -1584,12 +1599,12 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
         hook(idx);
         fence();
       }
-      if constexpr (ADD_SUM) l_run += sum_packed<T>(pk);
+      if constexpr (ADD_SUM) l_run = add_packed<T>(pk, l_run);
       rebase(max_with_other_half(mt));
     };
     // Reference exponent of the current tile (without a key mask every row
     // of a full tile has finite scores after tile 0).
-    auto ref_exp = [&]() __attribute__((always_inline)) -> float { return ceilf(m_run * c); };
+    auto ref_exp = [&]() __attribute__((always_inline)) -> float { return m_exp; };
 
     // Key tiles [kt0, kt1) of this workgroup: all of the query tile's, or one
     // chunk of them on the key-split grid.
@@ -1738,7 +1753,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<false, D>)) void attn_fwd_h16_
       } else {
         last_p(sb);
       }
-      l_run += sum_packed<T>(pk);
+      l_run = add_packed<T>(pk, l_run);
       pending = true;
       pend_live = NSB;
     }
