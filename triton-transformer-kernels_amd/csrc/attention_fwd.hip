@@ -268,20 +268,29 @@ __device__ __forceinline__ uint32_t lane_allowed(uint32_t sub_valid, int ks, int
   return a >> (4 * h);
 }
 
-__device__ __forceinline__ bool reg_allowed(uint32_t a, int r) {
-  return (a >> (8 * (r >> 2) + (r & 3))) & 1u;
-}
-
 // Sets scores of disallowed keys to -inf (tile of NSB sub-blocks from k0).
-template <int NSB, bool CAUSAL>
+// BITSEL: per register, a signed one-bit field extract of the allowed bit
+// gives an all-ones / all-zeros word and a bit-field insert selects the score
+// or -inf - two VALU instructions and no compare, so no VCC write that the
+// select has to wait for.  Otherwise a compare and a select per register
+// (fewer live registers where the kernel is at its register limit).
+template <int NSB, bool CAUSAL, bool BITSEL = true>
 __device__ __forceinline__ void apply_mask(f32x16 (&s)[NSB], int k0, uint64_t kvalid, int qrow, int h) {
 #pragma unroll
   for (int sb = 0; sb < NSB; ++sb) {
     const uint32_t a =
         lane_allowed<CAUSAL>(static_cast<uint32_t>(kvalid >> (32 * sb)), k0 + sb * 32, qrow, h);
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      if (!reg_allowed(a, r)) s[sb][r] = -INFINITY;
+    for (int r = 0; r < 16; ++r) {
+      const int bit = 8 * (r >> 2) + (r & 3);
+      if constexpr (BITSEL) {
+        const uint32_t keep = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int>(a), bit, 1));
+        const uint32_t bits = __float_as_uint(s[sb][r]);
+        s[sb][r] = __uint_as_float((bits & keep) | (0xff800000u & ~keep));
+      } else {
+        if (!((a >> bit) & 1u)) s[sb][r] = -INFINITY;
+      }
+    }
   }
 }
 
@@ -1045,7 +1054,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_short_kernel(AttnPar
     fence();
 
     // ---- softmax (exp2 domain, one tile: the running state starts empty) ----
-    if constexpr (MASKED) apply_mask<NSB, false>(s, 0, kv, qrow, h);
+    if constexpr (MASKED) apply_mask<NSB, false, false>(s, 0, kv, qrow, h);
     float mt = s[0][0];
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb)
