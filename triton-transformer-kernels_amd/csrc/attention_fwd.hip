@@ -30,7 +30,7 @@
 //       wavefront on the SIMD.
 //     - bf16/fp16: the 8-pass MFMA leaves the softmax as the bound (per
 //       64-key tile a wavefront issues 16 (head_dim 64) or 32 (128) MFMAs
-//       against ~140 VALU instructions, 32 of them v_exp_f32), so the loop
+//       against ~130 VALU instructions, 32 of them v_exp_f32), so the loop
 //       is software-pipelined.  Unmasked tiles run two phases per tile:
 //       Q.K of tile t+1 interleaved with the exp2 and 16-bit rounding of
 //       tile t's scores, then the P.V of tile t interleaved with the row max
