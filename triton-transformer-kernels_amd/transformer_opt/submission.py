@@ -54,7 +54,7 @@ from .dispatch import attention_forward
 from .kernels.gelu import gelu_
 from .kernels.residual_layer_norm import fused_residual_layer_norm, layer_norm
 from .model import TransformerBlock, TransformerConfig
-from .replay import CallTally, CapturedForward, ReplayCache, tensor_stamp
+from .replay import CapturedForward, ReplayCache
 
 __all__ = ["TransformerConfig", "UserOptimizedTransformer", "generate_random_case", "run_accuracy_tests"]
 
