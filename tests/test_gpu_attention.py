@@ -893,6 +893,35 @@ def test_key_split_schedule_matches_oracle_and_unsplit_launch(gpu_ready, batch, 
     assert contract_failures(whole.cpu(), reference) == 0
 
 
+@pytest.mark.parametrize("seq_len,dtype,causal,mask_mode", [
+    (4096, torch.bfloat16, True, "none"),
+    (4096, torch.float16, False, "prefix"),
+    (4097, torch.bfloat16, True, "none"),
+    (4097, torch.float16, True, "prefix"),
+    (4160, torch.float16, False, "prefix"),
+    (4223, torch.bfloat16, True, "prefix"),
+    (1024, torch.bfloat16, False, "none"),
+    (1025, torch.float16, False, "none"),
+    (2100, torch.bfloat16, False, "none"),
+])
+def test_head_dim_128_tile_size_switch(gpu_ready, seq_len, dtype, causal, mask_mode):
+    # 16-bit head_dim 128 runs 32-key tiles (three workgroups per CU) up to
+    # S = 4096 when causal or key-masked and up to 1024 otherwise, and 64-key
+    # tiles, two workgroups per CU, above that (without a workspace: no key
+    # split).  Both sides of each switch, with and without key masks, ragged
+    # last tiles of either size.
+    g = torch.Generator().manual_seed(seq_len + (7 if causal else 0))
+    shape = (2, seq_len, 1, 128)
+    q, k, v = (torch.randn(shape, generator=g).to(dtype) for _ in range(3))
+    mask = make_mask(mask_mode, 2, seq_len)
+    dev = torch.device("cuda")
+    with torch.inference_mode():
+        actual = _abi_attention(q.to(dev), k.to(dev), v.to(dev),
+                                None if mask is None else mask.to(dev), causal)
+    reference = oracle(q, k, v, mask, causal)
+    assert contract_failures(actual.cpu(), reference) == 0
+
+
 def test_key_split_workspace_rules(gpu_ready):
     # Too small a workspace runs the unsplit schedule (same result as no
     # workspace, bitwise); an unaligned one is rejected before any launch.
