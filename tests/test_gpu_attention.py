@@ -922,6 +922,30 @@ def test_head_dim_128_tile_size_switch(gpu_ready, seq_len, dtype, causal, mask_m
     assert contract_failures(actual.cpu(), reference) == 0
 
 
+@pytest.mark.parametrize("seq_len,dtype,mask_mode", [
+    (1024, torch.bfloat16, "none"),
+    (1025, torch.bfloat16, "none"),
+    (1000, torch.float16, "none"),
+    (2048, torch.float16, "prefix"),
+    (2049, torch.bfloat16, "prefix"),
+    (1500, torch.bfloat16, "prefix"),
+])
+def test_head_dim_64_causal_tile_size_switch(gpu_ready, seq_len, dtype, mask_mode):
+    # Causal 16-bit head_dim 64 runs 32-key tiles (four workgroups per CU)
+    # up to S = 1024, or 2048 with a key mask, and 64-key tiles above that
+    # (without a workspace: no key split).  Both sides of each switch.
+    g = torch.Generator().manual_seed(seq_len + 3)
+    shape = (2, seq_len, 2, 64)
+    q, k, v = (torch.randn(shape, generator=g).to(dtype) for _ in range(3))
+    mask = make_mask(mask_mode, 2, seq_len)
+    dev = torch.device("cuda")
+    with torch.inference_mode():
+        actual = _abi_attention(q.to(dev), k.to(dev), v.to(dev),
+                                None if mask is None else mask.to(dev), True)
+    reference = oracle(q, k, v, mask, True)
+    assert contract_failures(actual.cpu(), reference) == 0
+
+
 def test_key_split_workspace_rules(gpu_ready):
     # Too small a workspace runs the unsplit schedule (same result as no
     # workspace, bitwise); an unaligned one is rejected before any launch.
