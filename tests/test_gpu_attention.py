@@ -922,20 +922,25 @@ def test_head_dim_128_tile_size_switch(gpu_ready, seq_len, dtype, causal, mask_m
     assert contract_failures(actual.cpu(), reference) == 0
 
 
-@pytest.mark.parametrize("seq_len,dtype,mask_mode", [
-    (1024, torch.bfloat16, "none"),
-    (1025, torch.bfloat16, "none"),
-    (1000, torch.float16, "none"),
-    (2048, torch.float16, "prefix"),
-    (2049, torch.bfloat16, "prefix"),
-    (1500, torch.bfloat16, "prefix"),
+@pytest.mark.parametrize("seq_len,head_dim,dtype,mask_mode", [
+    (1024, 64, torch.bfloat16, "none"),
+    (1025, 64, torch.bfloat16, "none"),
+    (1000, 64, torch.float16, "none"),
+    (2048, 64, torch.float16, "prefix"),
+    (2049, 64, torch.bfloat16, "prefix"),
+    (1500, 64, torch.bfloat16, "prefix"),
+    (1024, 32, torch.bfloat16, "none"),
+    (1025, 32, torch.float16, "none"),
+    (333, 32, torch.bfloat16, "none"),
+    (700, 32, torch.float16, "prefix"),
 ])
-def test_head_dim_64_causal_tile_size_switch(gpu_ready, seq_len, dtype, mask_mode):
-    # Causal 16-bit head_dim 64 runs 32-key tiles (four workgroups per CU)
-    # up to S = 1024, or 2048 with a key mask, and 64-key tiles above that
-    # (without a workspace: no key split).  Both sides of each switch.
-    g = torch.Generator().manual_seed(seq_len + 3)
-    shape = (2, seq_len, 2, 64)
+def test_causal_small_head_dim_tile_size_switch(gpu_ready, seq_len, head_dim, dtype, mask_mode):
+    # Causal 16-bit head_dim 64 and 32 run 32-key tiles (four workgroups per
+    # CU) up to S = 1024 (head_dim 64 with a key mask: 2048) and 64-key
+    # tiles otherwise (without a workspace: no key split).  Both sides of
+    # each switch.
+    g = torch.Generator().manual_seed(seq_len + head_dim)
+    shape = (2, seq_len, 2, head_dim)
     q, k, v = (torch.randn(shape, generator=g).to(dtype) for _ in range(3))
     mask = make_mask(mask_mode, 2, seq_len)
     dev = torch.device("cuda")

@@ -1177,12 +1177,12 @@ __device__ __forceinline__ u16x4 lds_read_tr16(const unsigned short* p) {
 // shorter launches, where more resident wavefronts hide more latency than the
 // extra per-tile work costs.
 template <typename T, int D, bool CAUSAL, bool HAS_MASK, int BNK = 64>
-__global__ __launch_bounds__(kThreads, (BNK == 32 ? (D == 64 ? 4 : 3) : kMinWaves<false, D>)) void attn_fwd_h16_kernel(AttnParams p) {
+__global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWaves<false, D>)) void attn_fwd_h16_kernel(AttnParams p) {
   using C = H16Cfg<D, BNK>;
   constexpr int BN = C::BN, NSB = C::NSB, CPR = C::CPR, KS = C::KS,
                 NDB = C::NDB, VS = C::VS, VCH = C::VCH, G = C::G, NSTEP = C::NSTEP,
                 PDK = C::PDK, PDV = C::PDV;
-  static_assert(BNK == 64 || (BNK == 32 && (D == 64 || D == 128)), "32-key tiles are built for head_dim 64 and 128");
+  static_assert(BNK == 64 || (BNK == 32 && D >= 32), "32-key tiles are built for head_dim 32, 64 and 128");
   // The K region also stages the output tile (4 wavefronts x 32 rows of D + 8).
   constexpr int KBUF = (BN * KS > 64 * (D + 8)) ? BN * KS : 64 * (D + 8);
   __shared__ __attribute__((aligned(16))) unsigned short smK[2][KBUF];
@@ -2017,14 +2017,17 @@ hipError_t launch_d(int dtype, AttnParams& p, void* ws, int64_t ws_bytes, hipStr
       std::copy(sp.tab, sp.tab + sp.units, p.unit_tab);
     }
   }
-  if constexpr (D == 64 && CAUSAL) {
-    // 16-bit head_dim 64, causal, not key-split: 32-key tiles at four
-    // workgroups per CU up to S = 1024 (2048 with a key mask).  Measured
-    // against the 64-key kernel (same box, alternating): [16, 512, 16, 64]
-    // -13 %, [8, 1024, 16, 64] -4.5 %, key-masked fp16 [4, 2048, 16, 64]
-    // -2.5 %; config 4 (S = 2048, no mask) +6 %, [1, 8192, 16, 64] +12 %,
-    // and non-causal launches 6-9 % slower.
-    if (dtype != 0 && !p.split && p.S <= (HAS_MASK ? 2048 : 1024)) {
+  if constexpr ((D == 64 || D == 32) && CAUSAL) {
+    // 16-bit head_dim 64 and 32, causal, not key-split: 32-key tiles at four
+    // workgroups per CU up to S = 1024 (head_dim 64 with a key mask: 2048).
+    // Measured against the 64-key kernel (same box, alternating):
+    // [16, 512, 16, 64] -13 %, [8, 1024, 16, 64] -4.5 %, key-masked fp16
+    // [4, 2048, 16, 64] -2.5 %; config 4 (S = 2048, no mask) +6 %,
+    // [1, 8192, 16, 64] +12 %, non-causal launches 6-9 % slower.  Head dim
+    // 32: [32, 256, 16, 32] -15 %, [16, 512] -15 %, [8, 1024] -4 %, key-masked
+    // fp16 [8, 1024] +2.7 %.
+    const int bn32_max = HAS_MASK ? (D == 64 ? 2048 : 0) : 1024;
+    if (dtype != 0 && !p.split && p.S <= bn32_max) {
       const dim3 g(static_cast<unsigned>(p.units) * static_cast<unsigned>(p.BH)), blk(kThreads);
       if (dtype == 1) {
         attn_fwd_h16_kernel<BF16, D, CAUSAL, HAS_MASK, 32><<<g, blk, 0, stream>>>(p);
