@@ -619,6 +619,16 @@ def main() -> int:
             "tflops": round(tf, 2), "us": round(ms * 1e3, 2),
             "frac_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
         log(f"attention bf16 causal [4,2048,16,64]: {tf:.1f} TF ({ms * 1e3:.1f} us)")
+        # Shorter causal bf16 launches (the 32-key-tile kernels: three or four
+        # workgroups per CU).
+        short = {}
+        for b_, s_, d_ in ((16, 512, 64), (8, 1024, 64), (8, 1024, 128)):
+            tf, ms = attention_tflops(b_, s_, 16, d_, True, torch.bfloat16, steps=50, warmup=20)
+            short[f"B{b_}_S{s_}_H16_D{d_}"] = {
+                "tflops": round(tf, 2), "us": round(ms * 1e3, 2),
+                "frac_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
+        secondary["attention_bf16_causal_short_sequences"] = short
+        log(f"attention bf16 causal short sequences: {short}")
         us = packed_attention_5b_us()
         tf = attention_flops(512, 8, 64, 64, False) / (us * 1e-6) / 1e12
         secondary["attention_fp32_noncausal_B512_H8_S64_D64_packed"] = {
