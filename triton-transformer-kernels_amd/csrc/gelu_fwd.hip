@@ -9,7 +9,10 @@
 // benchmarks/torch_transformer_benchmark.py:95-97).
 //
 // HBM-bound: a lane moves 16-byte vectors (8 bf16/fp16 or 4 fp32 values),
-// kUnroll of them per pass, all loads issued before any store.  Loads are
+// kUnroll of them per pass, all loads issued before any store.  One vector
+// per lane (the most workgroups in flight) measured fastest over inputs that
+// exceed the 256 MB MALL: bf16 [8192, 4096] 28.5 / 25.3 / 23.8 us and fp32
+// [32768, 2048] 95.5 / 94.4 / 90.6 us with 4 / 2 / 1 vectors per lane.  Loads are
 // non-temporal; stores are ordinary, because the next GEMM reads the result
 // right away and should find it in the caches (non-temporal stores made the
 // config-4 encoder 0.8 % slower).  y == x (in place) is allowed:
@@ -21,7 +24,7 @@ namespace ttk {
 namespace {
 
 constexpr int kGeluThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;
 
 __device__ __forceinline__ u32x4 gelu_vec(F32, u32x4 raw) {
   u32x4 out;
