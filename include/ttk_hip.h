@@ -25,7 +25,11 @@
 extern "C" {
 #endif
 
-#define TTK_ABI_VERSION 6
+#define TTK_ABI_VERSION 7
+
+/* Bytes of the arrival-counter block that leads every attention workspace
+ * (and the library's static scratch): the same for every launch shape. */
+#define TTK_ATTENTION_WS_COUNTER_BYTES 16384
 
 typedef enum {
   TTK_OK = 0,
@@ -93,10 +97,11 @@ size_t ttk_attention_workspace_size(int dtype, int64_t B, int64_t S, int64_t H,
 
 /*
  * ttk_attention_fwd with a caller-owned workspace (256-byte aligned,
- * workspace_bytes long).  The workspace starts with the arrival counters of
- * the schedule, B * H * ceil(S / 128) * 4 bytes rounded up to a multiple of
- * 256; those must be zero before the first call, and every call leaves them
- * zero.  The rest needs no initialisation.
+ * workspace_bytes long).  The workspace starts with the schedule's arrival
+ * counters, a block of TTK_ATTENTION_WS_COUNTER_BYTES whatever the shape;
+ * those must be zero before the first call, and every call leaves them zero,
+ * so one workspace serves launches of any shapes in any order.  The rest
+ * needs no initialisation.
  *
  * With at least ttk_attention_workspace_size() bytes, a causal bf16/fp16
  * launch whose heaviest query tile outweighs 1.5 average workgroup slots

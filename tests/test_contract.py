@@ -28,11 +28,35 @@ def _cpu_qkv(dtype=torch.float32):
     return q, torch.randn_like(q), torch.randn_like(q)
 
 
-def test_backends_name_only_the_hip_route():
+def test_backends_are_the_hip_routes_and_the_explicit_reference():
     # "triton" is the reference's forced fused route (config.py:11,
     # dispatch.py:119-132); here it names the HIP kernel that replaces it.
-    assert ATTENTION_BACKENDS == ("auto", "hip", "triton")
+    # "reference" is the reference's explicit-math route (dispatch.py:69-96).
+    assert ATTENTION_BACKENDS == ("auto", "hip", "triton", "reference")
     assert triton_attention_support is hip_attention_support
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_route_is_the_explicit_math(dtype, causal):
+    # Forced only: recorded as "reference", plain torch operations (it runs
+    # here on the CPU), equal to the oracle's restatement of the reference's
+    # explicit attention (dispatch.py:69-96) on the same inputs, all-masked
+    # rows NaN as there.
+    from oracle.attention import explicit_attention as oracle_explicit
+
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(2, 37, 3, 16, generator=g, dtype=dtype) for _ in range(3))
+    mask = torch.arange(37)[None, :] < torch.tensor([[37], [20]])
+    out, record = attention_forward(q, k, v, mask, causal=causal, scale=0.3, backend="reference")
+    assert (record.requested, record.selected) == ("reference", "reference")
+    expected = oracle_explicit(q, k, v, mask, causal, 0.3)
+    assert out.shape == q.shape and out.dtype == dtype and out.is_contiguous()
+    torch.testing.assert_close(out, expected, rtol=1e-6, atol=1e-6)
+    empty = torch.zeros(2, 37, dtype=torch.bool)
+    empty[0] = True
+    out, _ = attention_forward(q, k, v, empty, causal=causal, backend="reference")
+    assert bool(out[1].isnan().all()) and bool(out[0].isfinite().all())
 
 
 def test_invalid_backend_is_rejected():
@@ -114,10 +138,11 @@ def test_model_constructor_validation_and_state_surface():
         UserOptimizedTransformer(cfg, execution_mode="invalid")
     with pytest.raises(ValueError, match="attention_backend"):
         UserOptimizedTransformer(cfg, attention_backend="sdpa")
-    forced = UserOptimizedTransformer(cfg, attention_backend="triton").eval()
-    assert forced._replay_refusal(torch.randn(1, 128, 128), None) == "attention backend is forced"
+    for backend in ("triton", "reference"):
+        forced = UserOptimizedTransformer(cfg, attention_backend=backend).eval()
+        assert forced._replay_refusal(torch.randn(1, 128, 128), None) == "attention backend is forced"
     model = UserOptimizedTransformer(cfg).eval()
-    assert model.attention_backend_counts == {"hip": 0}
+    assert model.attention_backend_counts == {"hip": 0, "reference": 0}
     assert model.fused_residual_layer_norm_calls == 0 and model.cuda_graph_replays == 0
     cloned = copy.deepcopy(model)
     assert cloned.state_dict().keys() == model.state_dict().keys()

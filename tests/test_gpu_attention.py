@@ -156,6 +156,32 @@ def test_forced_triton_backend_runs_the_hip_kernel(gpu_ready):
         attention_forward(bad, bad, bad, backend="triton")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_reference_route_runs_the_explicit_math_on_the_gpu(gpu_ready, dtype):
+    # backend="reference" (reference dispatch.py:69-96, 145-152): explicit
+    # torch math on the device, never the kernel.  fp32 agrees with the
+    # oracle's restatement on the CPU within float32 rounding; bf16/fp16
+    # (scores and probabilities rounded to 8 / 11 bits, as in the reference)
+    # within the model-level bound, and with the HIP kernel within it too.
+    from oracle.attention import explicit_attention as oracle_explicit
+    from transformer_opt import attention_forward
+
+    g = torch.Generator().manual_seed(17)
+    q, k, v = (torch.randn(2, 150, 4, 64, generator=g).to(dtype) for _ in range(3))
+    mask = make_mask("prefix", 2, 150)
+    with torch.inference_mode():
+        out, record = attention_forward(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), causal=True,
+                                        backend="reference")
+        hip, _ = attention_forward(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), causal=True,
+                                   backend="hip")
+    assert (record.requested, record.selected) == ("reference", "reference")
+    expected = oracle_explicit(q.float(), k.float(), v.float(), mask, True)
+    atol, rtol = (1e-5, 1e-5) if dtype == torch.float32 else (5e-2, 5e-2)
+    for got in (out, hip):
+        err = (got.float().cpu() - expected).abs()
+        assert bool(((err <= atol) | (err <= rtol * expected.abs())).all()), float(err.max())
+
+
 def oracle(q, k, v, mask, causal, scale=None):
     """The checker of each dtype, on the (already rounded) inputs.
 
@@ -188,6 +214,70 @@ def test_hip_attention_matches_explicit_reference(
         failures = contract_failures(actual, reference)
         assert failures == 0, f"seed={seed} contract failures={failures}"
         tight_check(actual, reference, dtype)
+
+
+def reference_math_bound_failures(actual, q, k, v, mask, causal, scale=None) -> int:
+    """Elements of a 16-bit kernel output outside the rounding bound of the
+    reference's explicit math, evaluated in fp32 on the same rounded inputs.
+
+    The reference (dispatch.py:69-96) on fp32 copies of q/k/v gives
+    out = sum(p v) / sum(p).  The 16-bit kernel differs from it by (1) the
+    rounding of each probability to the input dtype before P.V, w = p(1+e),
+    |e| <= u, which moves the output by at most 2u/(1-u) * sum(p|v|)/sum(p)
+    (the closed form pinned on the CPU by test_p_rounding_error_is_within_
+    its_closed_form_bound), (2) the rounding of the output to the input dtype,
+    at most u * |out|, and (3) fp32 summation order, covered by 2e-3.  u is
+    the unit roundoff: 2^-8 (bf16), 2^-11 (fp16).  Rows with no allowed key
+    are 0 in both (the kernel contract).
+    """
+    q32, k32, v32 = q.float(), k.float(), v.float()
+    if q.shape[0] * q.shape[2] * q.shape[1] ** 2 > (1 << 26):
+        ref = chunked_kernel_contract_attention(q32, k32, v32, mask, causal, scale)
+        mag = chunked_kernel_contract_attention(q32, k32, v32.abs(), mask, causal, scale)
+        batch, seq_len, heads, head_dim = q.shape
+        ref = ref.view(batch, heads, seq_len, head_dim).transpose(1, 2)
+        mag = mag.view(batch, heads, seq_len, head_dim).transpose(1, 2)
+    else:
+        ref = kernel_contract_attention(q32, k32, v32, mask, causal, scale)
+        mag = kernel_contract_attention(q32, k32, v32.abs(), mask, causal, scale)
+    unit = 2.0 ** -8 if q.dtype == torch.bfloat16 else 2.0 ** -11
+    bound = 2e-3 + 2 * unit / (1 - unit) * mag + unit * ref.abs()
+    err = (actual.float().cpu() - ref).abs()
+    return int((~(err <= bound)).sum())
+
+
+SIXTEEN_BIT_CASES = [c for c in CASES if c[4] != torch.float32] + [
+    (1, 4096, 2, 64, torch.bfloat16, True, "none", 1.0),
+    (2, 1000, 3, 128, torch.float16, False, "prefix", 2.0),
+]
+
+
+@pytest.mark.parametrize("batch,seq_len,heads,head_dim,dtype,causal,mask_mode,input_scale",
+                         SIXTEEN_BIT_CASES)
+def test_16bit_attention_within_rounding_bound_of_reference_math(
+    gpu_ready, batch, seq_len, heads, head_dim, dtype, causal, mask_mode, input_scale
+):
+    # The 16-bit kernels against the reference's own explicit math (not the
+    # kernel-rounding oracle): fp32 attention on the rounded inputs, held to
+    # the closed-form bound of the two roundings a 16-bit kernel performs.
+    g = torch.Generator().manual_seed(seq_len * 3 + head_dim)
+    shape = (batch, seq_len, heads, head_dim)
+    q = (torch.randn(shape, generator=g) * input_scale).to(dtype)
+    k = (torch.randn(shape, generator=g) * input_scale).to(dtype)
+    v = torch.randn(shape, generator=g).to(dtype)
+    mask = make_mask(mask_mode, batch, seq_len)
+    actual = run_hip(q, k, v, mask, causal)
+    assert reference_math_bound_failures(actual, q, k, v, mask, causal) == 0
+
+
+def test_16bit_config4_attention_within_rounding_bound_of_reference_math(gpu_ready):
+    # Config 4's attention (B=4, S=2048, H=16, D=64, causal, bf16), every
+    # element of every head against the reference's explicit math.
+    g = torch.Generator().manual_seed(44)
+    shape = (4, 2048, 16, 64)
+    q, k, v = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(3))
+    actual = run_hip(q, k, v, None, True)
+    assert reference_math_bound_failures(actual, q, k, v, None, True) == 0
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -885,8 +975,7 @@ def test_key_split_schedule_matches_oracle_and_unsplit_launch(gpu_ready, batch, 
         again = _abi_attention(qd, kd, vd, md, True, workspace)
         whole = _abi_attention(qd, kd, vd, md, True)
     torch.cuda.synchronize()
-    counters = -(-batch * heads * (-(-seq_len // 128)) * 4 // 256) * 256
-    assert int(workspace[:counters].count_nonzero()) == 0
+    assert int(workspace[:_native.ATTENTION_WS_COUNTER_BYTES].count_nonzero()) == 0
     assert torch.equal(split, again)
     reference = oracle(q, k, v, mask, True)
     assert contract_failures(split.cpu(), reference) == 0
@@ -949,6 +1038,72 @@ def test_causal_small_head_dim_tile_size_switch(gpu_ready, seq_len, head_dim, dt
                                 None if mask is None else mask.to(dev), True)
     reference = oracle(q, k, v, mask, True)
     assert contract_failures(actual.cpu(), reference) == 0
+
+
+# Split shapes in an order whose split plans grow and then shrink (more
+# split slots, larger partial states, then fewer): each launch finds the
+# previous launch's partial states in the workspace.
+SPLIT_SEQUENCE = [
+    (1, 2048, 2, 64, torch.bfloat16),
+    (1, 4096, 4, 64, torch.bfloat16),
+    (1, 4096, 4, 128, torch.bfloat16),
+    (1, 4096, 16, 32, torch.float16),
+    (2, 4096, 4, 64, torch.bfloat16),
+    (1, 1024, 2, 64, torch.float16),
+]
+
+
+def _split_inputs(shape, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn(shape, generator=g).to(dtype) for _ in range(3))
+
+
+def test_key_split_one_workspace_across_shapes(gpu_ready):
+    # One caller workspace, sized for the largest plan, serves every shape in
+    # turn: each split launch equals the same launch on a fresh zero-filled
+    # workspace bitwise, and the counter block is zero after every launch.
+    from transformer_opt import _native
+
+    lib = _native.load()
+    sizes = []
+    for (b, s, h, d, dtype) in SPLIT_SEQUENCE:
+        code = 1 if dtype == torch.bfloat16 else 2
+        sizes.append(lib.ttk_attention_workspace_size(code, b, s, h, d, 1))
+        assert sizes[-1] > 0, (b, s, h, d)
+    shared = torch.zeros(max(sizes), dtype=torch.uint8, device="cuda")
+    for i, (b, s, h, d, dtype) in enumerate(SPLIT_SEQUENCE):
+        q, k, v = (t.cuda() for t in _split_inputs((b, s, h, d), dtype, 40 + i))
+        with torch.inference_mode():
+            got = _abi_attention(q, k, v, None, True, shared)
+            fresh = _abi_attention(q, k, v, None, True,
+                                   torch.zeros(sizes[i], dtype=torch.uint8, device="cuda"))
+        torch.cuda.synchronize()
+        assert torch.equal(got, fresh), (b, s, h, d)
+        assert int(shared[:_native.ATTENTION_WS_COUNTER_BYTES].count_nonzero()) == 0
+
+
+def test_key_split_through_the_wrapper_across_shapes(gpu_ready):
+    # The product wrapper keeps one workspace per stream and reuses it for
+    # every shape: its outputs equal fresh-workspace launches bitwise, and
+    # the smaller shapes stay within the oracle's bound.
+    from transformer_opt.kernels.attention import hip_attention
+    from transformer_opt import _native
+
+    lib = _native.load()
+    for i, (b, s, h, d, dtype) in enumerate(SPLIT_SEQUENCE):
+        cpu = _split_inputs((b, s, h, d), dtype, 60 + i)
+        q, k, v = (t.cuda() for t in cpu)
+        code = 1 if dtype == torch.bfloat16 else 2
+        nbytes = lib.ttk_attention_workspace_size(code, b, s, h, d, 1)
+        with torch.inference_mode():
+            got = hip_attention(q, k, v, causal=True)
+            fresh = _abi_attention(q, k, v, None, True,
+                                   torch.zeros(nbytes, dtype=torch.uint8, device="cuda"))
+        torch.cuda.synchronize()
+        assert torch.equal(got, fresh), (b, s, h, d)
+        if s * h <= 8192:
+            reference = oracle(*cpu, None, True)
+            assert contract_failures(got.cpu(), reference) == 0, (b, s, h, d)
 
 
 def test_key_split_workspace_rules(gpu_ready):

@@ -170,11 +170,11 @@ def test_counters_count_forwards_not_warmups(gpu_ready):
             model(x, mask)
     layers = CFG.num_layers
     assert model.cuda_graph_replays == 3
-    assert model.attention_backend_counts == {"hip": 3 * layers}
+    assert model.attention_backend_counts == {"hip": 3 * layers, "reference": 0}
     assert model.fused_residual_layer_norm_calls == 3 * 2 * layers
     model.reset_attention_backend_counts()
     assert (model.attention_backend_counts, model.fused_residual_layer_norm_calls,
-            model.cuda_graph_replays) == ({"hip": 0}, 0, 0)
+            model.cuda_graph_replays) == ({"hip": 0, "reference": 0}, 0, 0)
 
 
 # (why the call stays eager, how the call is made, expected refusal)
@@ -232,7 +232,7 @@ def test_input_rules_keep_calls_eager(gpu_ready):
         with torch.inference_mode():
             assert forced._replay_refusal(x, None) == refusal
             assert torch.equal(forced(x), eager(x))
-            assert forced.attention_backend_counts == {"hip": CFG.num_layers}
+            assert forced.attention_backend_counts == {"hip": CFG.num_layers, "reference": 0}
 
 
 def test_least_recently_used_capture_is_evicted(gpu_ready):
@@ -300,3 +300,26 @@ def test_replay_is_bitwise_eager_across_dtypes(gpu_ready, dtype, cfg, masked):
             torch.cuda.synchronize()
             assert torch.equal(out, reference), (dtype, step)
     assert model.cuda_graph_replays == 4
+
+
+def test_replay_of_a_key_split_attention_is_bitwise_eager(gpu_ready):
+    # A causal bf16 encoder whose attention takes the key-split schedule
+    # (B=1, S=4096, H=4, head_dim 64): under capture its workspace comes from
+    # the graph pool and its counter block is cleared inside the graph, so
+    # every replay - with eager split launches on the same stream in
+    # between, which reuse the stream's own workspace - equals the eager twin.
+    from transformer_opt import _native
+
+    cfg = TransformerConfig(1, 4096, 256, 4, 512, 2, True)
+    assert _native.load().ttk_attention_workspace_size(1, 1, 4096, 4, 64, 1) > 0
+    model, eager = twin(cfg, torch.bfloat16, seed=4)
+    with torch.inference_mode():
+        for step in range(3):
+            x = sample(cfg, torch.bfloat16, seed=30 + step)
+            out = model(x)
+            torch.cuda.synchronize()
+            reference = eager(x)
+            torch.cuda.synchronize()
+            assert torch.equal(out, reference), step
+    assert model.cuda_graph_replays == 3
+    assert model._inference_graph is not None

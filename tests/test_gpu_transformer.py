@@ -57,8 +57,31 @@ def test_optimized_matches_baseline(gpu_ready, shape, causal, padding):
     res = compare_outputs(ref, out, rtol=0.01, atol=0.001)
     assert res.passed, (f"failed={res.failed_elements}/{res.total_elements} max_abs={res.max_abs_error:.3e} "
                         f"at {res.worst_index}")
-    assert model.attention_backend_counts == {"hip": layers}
+    assert model.attention_backend_counts == {"hip": layers, "reference": 0}
     assert model.fused_residual_layer_norm_calls == 2 * layers
+
+
+@pytest.mark.parametrize("causal,padding", [(False, 0.0), (True, 0.3)])
+def test_forced_reference_route_model(gpu_ready, causal, padding):
+    # The reference's forced comparison route (its tests/test_gpu_attention.py:
+    # 107, 146, 166 force backend="reference"): the model runs eager, every
+    # attention on the dispatcher's explicit-math route, counted under
+    # "reference"; the output matches the oracle model and the HIP-attention
+    # model under the organizer's rule.
+    cfg = TransformerConfig(2, 96, 256, 4, 512, 2, causal)
+    baseline, model = build(cfg, backend="reference")
+    _, hip_model = build(cfg)
+    x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 11, padding, 1.0)
+    with torch.inference_mode():
+        ref = baseline(x, mask)
+        xd, md = x.cuda(), None if mask is None else mask.cuda()
+        out = model(xd, md)
+        hip = hip_model(xd, md)
+    for candidate in (out, hip):
+        res = compare_outputs(ref, candidate, rtol=0.01, atol=0.001)
+        assert res.passed, f"failed={res.failed_elements} max_abs={res.max_abs_error:.3e}"
+    assert model.attention_backend_counts == {"hip": 0, "reference": 2}
+    assert model.cuda_graph_replays == 0
 
 
 @pytest.mark.parametrize("seed,scale,padding", [(1234, 0.25, 0.0), (2026, 1.0, 0.25), (4096, 4.0, 0.0)])

@@ -907,7 +907,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_short_kernel(AttnPar
 
   // Every global access is a buffer access whose resource covers exactly the
   // rows < S of one head (the host checks row stride >= head_dim and that
-  // offsets stay below 2^31): rows past S read as zeros and are not written,
+  // the offsets of all 64 rows a lane may address stay below 2^31): rows past
+  // S read as zeros and are not written,
   // without a branch.  The range check covers the VGPR offset (plus the
   // instruction offset) but not soffset, so the row part of every offset is
   // in the VGPR.  The loads of the next item are issued unconditionally -
@@ -1823,7 +1824,7 @@ __global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWave
       }
       vm_wait();
       __syncthreads();
-      int* const counter = &p.ws_cnt[w.bh * p.nq + qb];
+      int* const counter = &p.ws_cnt[slot];
       int* arrival = reinterpret_cast<int*>(&smV[0][0]);  // V buffers are idle now
       if (tid == 0) {
         *arrival = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -1976,9 +1977,12 @@ SplitPlan plan_key_split(int dtype, int D, bool causal, int64_t BH, int64_t S) {
   }
   const int64_t nv = ((D + 31) / 32) * 16 + 2;  // floats of partial state per lane
   const int64_t split_tiles = nq - q0;
+  // One counter per split slot (batch, head, split query tile), in the fixed
+  // block that leads every workspace.
+  if (BH * split_tiles > kSplitCounterSlots) return SplitPlan{};
   sp.q0 = q0;
   sp.units = nu;
-  sp.cnt_bytes = (BH * nq * 4 + 255) / 256 * 256;  // one counter per (batch, head, query tile)
+  sp.cnt_bytes = kSplitCounterBytes;
   sp.bytes = sp.cnt_bytes + BH * split_tiles * sp.maxch * 4 * nv * 64 * 4;
   sp.on = true;
   return sp;
@@ -2058,12 +2062,14 @@ hipError_t launch_d(int dtype, AttnParams& p, void* ws, int64_t ws_bytes, hipStr
     }
   }
   if constexpr (!CAUSAL && (D == 32 || D == 64)) {
-    // Its buffer resources span rows 0..S-1 of one head: rows must not
-    // overlap (sequence stride >= head_dim) and the span must stay below 2^31
-    // bytes, or rows past S would not read as zeros.
-    auto span_ok = [&](int64_t rs) { return rs >= D && ((p.S - 1) * rs + D) * 4 < (int64_t{1} << 31); };
+    // Its buffer resources span rows 0..S-1 of one head, and its lanes
+    // address rows 0..63 (rows past S are padding) with 32-bit offsets: rows
+    // must not overlap (sequence stride >= head_dim) and the offset of every
+    // padded row must stay below 2^31 bytes, or it could wrap back inside the
+    // resource instead of reading as zero (or being dropped, for stores).
+    auto span_ok = [&](int64_t rs) { return rs >= D && (63 * rs + D) * 4 < (int64_t{1} << 31); };
     if (dtype == 0 && p.S <= 64 && span_ok(p.qs) && span_ok(p.ks) && span_ok(p.vs) && span_ok(p.os) &&
-        (p.S - 1) * p.ms < (int64_t{1} << 31) - 1) {
+        63 * p.ms < (int64_t{1} << 31) - 1) {
       // Short sequences: one wavefront per (batch, head, 32-query half), a
       // persistent grid of two workgroups per CU (fewer when there are fewer
       // items than wavefronts).

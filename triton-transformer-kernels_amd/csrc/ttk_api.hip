@@ -40,6 +40,9 @@ int elem_bytes(int dtype) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+static_assert(ttk::kSplitCounterBytes == TTK_ATTENTION_WS_COUNTER_BYTES,
+              "the counter block of the header is the kernels' one");
+
 // HIP launches at most 2^32 - 1 work-items per grid dimension; every kernel
 // here runs 256-thread workgroups on a 1-D grid.
 constexpr int64_t kMaxGroups = int64_t{0xFFFFFFFF} / 256;

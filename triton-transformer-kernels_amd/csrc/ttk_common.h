@@ -98,16 +98,24 @@ struct AttnParams {
   // head) runs query tile unit_tab[u] & 1023, chunk (unit_tab[u] >> 10) & 7
   // of ((unit_tab[u] >> 13) + 1).  Chunks of query tiles >= split_q0 leave
   // their partial state in ws_part and count themselves in ws_cnt; the last
-  // one to arrive merges the partials and writes the rows.
+  // one to arrive merges the partials and writes the rows.  Both are indexed
+  // by the split slot bh * split_tiles + (query tile - split_q0).
   int split;
   int split_q0;
   int split_tiles;   // nq - split_q0
   int split_maxch;   // chunks of the heaviest query tile
-  int* ws_cnt;       // [BH * nq] arrival counters, zero between launches
+  int* ws_cnt;       // [kSplitCounterSlots] arrival counters, zero between launches
   float* ws_part;    // [BH * split_tiles * split_maxch * 4 waves * lanes * state]
   unsigned short unit_tab[256];
 };
 constexpr int kMaxSplitUnits = 256;
+// The key-split workspace starts with a counter block of fixed size, the
+// same for every shape, so a launch never finds another launch's partial
+// states where its counters are: the block is zero before the first launch
+// and every launch leaves it zero.  A plan with more split slots than the
+// block holds runs unsplit.
+constexpr int kSplitCounterSlots = 4096;
+constexpr int64_t kSplitCounterBytes = int64_t{kSplitCounterSlots} * 4;
 
 // Launch parameters of the residual + LayerNorm kernels.
 struct LnParams {

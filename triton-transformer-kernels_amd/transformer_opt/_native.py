@@ -36,7 +36,10 @@ EXPORTED_SYMBOLS = (
     "ttk_residual_layernorm_fwd",
     "ttk_gelu_fwd",
 )
-ABI_VERSION = 6
+ABI_VERSION = 7
+# TTK_ATTENTION_WS_COUNTER_BYTES: the zero-initialised counter block that
+# leads every attention workspace, the same for every launch shape.
+ATTENTION_WS_COUNTER_BYTES = 16384
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -5,11 +5,12 @@ Mirrors the reference's ``transformer_opt/config.py``: the same Q/K/V contract
 that explains every refusal (reference ``triton_attention_support``,
 config.py:143-175).  What changes is the envelope of the hardware path:
 
-* backends are ``auto``, ``hip`` and ``triton``, and all three run the HIP
-  kernel: ``triton`` is the reference's name for its forced fused route
-  (config.py:11, dispatch.py:119-132), kept so callers that force it land on
-  the kernel that replaces it.  There is no SDPA or explicit-math route in
-  the product path;
+* backends are ``auto``, ``hip``, ``triton`` and ``reference``.  The first
+  three run the HIP kernel: ``triton`` is the reference's name for its
+  forced fused route (config.py:11, dispatch.py:119-132), kept so callers
+  that force it land on the kernel that replaces it.  ``reference`` is the
+  reference's explicit-math route, run only when named, never by ``auto``.
+  There is no SDPA route;
 * dtypes are fp32, bf16 and fp16 (the reference stopped at fp16/fp32,
   config.py:17-18);
 * sequence length is bounded by the kernel's index range, not by a measured
@@ -25,8 +26,8 @@ from typing import Optional
 
 import torch
 
-ATTENTION_BACKENDS = ("auto", "hip", "triton")
-# Backends a caller may force; each names the HIP kernel.
+ATTENTION_BACKENDS = ("auto", "hip", "triton", "reference")
+# Forced backends that name the HIP kernel.
 FORCED_BACKENDS = frozenset({"hip", "triton"})
 SUPPORTED_HEAD_DIMS = frozenset({8, 16, 32, 64, 128})
 SUPPORTED_DTYPES = frozenset({torch.float32, torch.bfloat16, torch.float16})

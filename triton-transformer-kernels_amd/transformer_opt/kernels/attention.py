@@ -9,6 +9,7 @@ current stream.  Unsupported inputs raise; nothing falls back.
 from __future__ import annotations
 
 import threading
+from collections import OrderedDict
 from typing import Optional
 
 import torch
@@ -29,7 +30,12 @@ def hip_available() -> bool:
 
 
 _WS_SIZES: dict = {}
-_WORKSPACES: dict = {}
+# One workspace per (device, stream), most recently used last; at most
+# _MAX_WORKSPACES are kept.  Dropping one is safe: its memory returns to the
+# caching allocator of the stream it was allocated and used on, behind that
+# stream's pending launches.
+_WORKSPACES: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_MAX_WORKSPACES = 8
 _WS_LOCK = threading.Lock()
 
 
@@ -44,28 +50,33 @@ def _workspace_bytes(lib, dtype_code: int, batch: int, seq_len: int, heads: int,
     return nbytes
 
 
-def _workspace(device: torch.device, nbytes: int, counter_bytes: int) -> Optional[torch.Tensor]:
+def _workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
     """Workspace of the key-split attention schedule for the current stream.
 
-    Its arrival counters must be zero before a launch, and every launch
-    leaves them zero.  Outside graph capture each (device, stream) keeps one
-    zero-filled buffer, grown when a launch needs more; launches on one
-    stream never overlap.  During a capture the buffer comes from the
-    graph's memory pool and its counters are cleared inside the graph (a
-    fill kernel, not a memset node), so every replay starts from zero.
+    It starts with a fixed block of arrival counters (the same bytes for
+    every launch shape) that must be zero before a launch; every launch
+    leaves it zero, and the partial states after it need no initialisation,
+    so one buffer serves launches of any shapes in any order.  Outside graph
+    capture each (device, stream) keeps one zero-filled buffer, replaced by a
+    larger zero-filled one when a launch needs more; launches on one stream
+    never overlap.  During a capture the buffer comes from the graph's
+    memory pool and its counters are cleared inside the graph (a fill
+    kernel, not a memset node), so every replay starts from zero.
     """
     if nbytes == 0:
         return None
     if torch.cuda.is_current_stream_capturing():
         ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        ws[:counter_bytes].zero_()
+        ws[:_native.ATTENTION_WS_COUNTER_BYTES].zero_()
         return ws
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     with _WS_LOCK:
-        ws = _WORKSPACES.get(key)
+        ws = _WORKSPACES.pop(key, None)
         if ws is None or ws.numel() < nbytes:
             ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-            _WORKSPACES[key] = ws
+        _WORKSPACES[key] = ws
+        while len(_WORKSPACES) > _MAX_WORKSPACES:
+            _WORKSPACES.popitem(last=False)
     return ws
 
 
@@ -127,10 +138,7 @@ def hip_attention(
     with torch.cuda.device(q.device):
         nbytes = _workspace_bytes(lib, dtype_code, batch, seq_len, num_heads, head_dim, causal,
                                   q.device.index)
-        # The counters lead the workspace: 4 bytes per (batch, head, 128-query
-        # tile), rounded up to 256.
-        counter_bytes = min(nbytes, -(-batch * num_heads * (-(-seq_len // 128)) * 4 // 256) * 256)
-        ws = _workspace(q.device, nbytes, counter_bytes)
+        ws = _workspace(q.device, nbytes)
         stream = torch.cuda.current_stream(q.device).cuda_stream
         status = lib.ttk_attention_fwd_ws(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), mask_ptr, out.data_ptr(),

@@ -30,7 +30,10 @@ How a forward runs here:
 What is MI355X-specific: every attention runs on the HIP kernel (fp32,
 bf16, fp16) and every LayerNorm on the HIP residual + LayerNorm kernel - the
 reference's per-shape routing between Triton, SDPA and explicit math
-(submission.py:235-321) is gone, and so is the SDPA counter; the packed QKV
+(submission.py:235-321) is gone, and so is the SDPA counter.  The counters
+are ``{"hip": n, "reference": n}``: a model built with
+``attention_backend="reference"`` runs the explicit-math attention route of
+the dispatcher (never chosen otherwise) and counts it there; the packed QKV
 projection is used for every width and dtype (submission.py:184-190
 restricted it); graph replay is eligible for every supported shape and dtype
 instead of a measured shape set (submission.py:582-590), with up to
@@ -219,7 +222,7 @@ class UserOptimizedTransformer(nn.Module):
         self.attention_backend = attention_backend
         self.execution_mode = execution_mode
         self.cuda_graph_replays = 0
-        self.attention_backend_counts: Dict[str, int] = {"hip": 0}
+        self.attention_backend_counts: Dict[str, int] = {"hip": 0, "reference": 0}
         self.fused_residual_layer_norm_calls = 0
         # Captures, packed projections and the lock: derived inference state,
         # outside the state dict and not copied with the module.
@@ -244,7 +247,7 @@ class UserOptimizedTransformer(nn.Module):
         return dict(self._replay.packs)
 
     def reset_attention_backend_counts(self) -> None:
-        self.attention_backend_counts = {"hip": 0}
+        self.attention_backend_counts = {"hip": 0, "reference": 0}
         self.fused_residual_layer_norm_calls = 0
         self.cuda_graph_replays = 0
 
@@ -343,13 +346,20 @@ class UserOptimizedTransformer(nn.Module):
         mask = valid_token_mask
         if mask is not None and not mask.is_contiguous():
             mask = mask.contiguous()
-        return self._encode(self._operands(), x.contiguous(), mask, _ModelTally(self))
+        # Operand resolution updates the shared cache: under the lock, like
+        # every capture and replay; the eager forward itself runs outside it.
+        with self._replay.lock:
+            ops = self._operands()
+        return self._encode(ops, x.contiguous(), mask, _ModelTally(self))
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self._replay_refusal(x, valid_token_mask) is None:
-            ops = self._operands()
-            if ops.fingerprint is not None:
-                return self._replay_forward(ops, x, valid_token_mask)
+            # Resolve, fingerprint and replay under one hold of the lock, so
+            # another thread cannot move the cached operands in between.
+            with self._replay.lock:
+                ops = self._operands()
+                if ops.fingerprint is not None:
+                    return self._replay_forward(ops, x, valid_token_mask)
         return self._forward_eager(x, valid_token_mask)
 
     # -- graph replay -------------------------------------------------------------
@@ -374,8 +384,10 @@ class UserOptimizedTransformer(nn.Module):
         return result
 
     def _can_replay_cuda_graph(self, x, valid_token_mask) -> bool:
-        return (self._replay_refusal(x, valid_token_mask) is None
-                and self._operands().fingerprint is not None)
+        if self._replay_refusal(x, valid_token_mask) is not None:
+            return False
+        with self._replay.lock:
+            return self._operands().fingerprint is not None
 
     def _replay_refusal(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> Optional[str]:
         """The first rule that keeps this call eager, or None if it may replay.
