@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define TTK_ABI_VERSION 7
+#define TTK_ABI_VERSION 8
 
 /* Bytes of the arrival-counter block that leads every attention workspace
  * (and the library's static scratch): the same for every launch shape. */
@@ -39,6 +39,9 @@ typedef enum {
 } ttk_status;
 
 typedef enum { TTK_F32 = 0, TTK_BF16 = 1, TTK_F16 = 2 } ttk_dtype;
+
+/* Activation applied by ttk_linear_fwd to the rounded linear output. */
+typedef enum { TTK_ACT_NONE = 0, TTK_ACT_GELU = 1 } ttk_activation;
 
 /* Version of this ABI (TTK_ABI_VERSION of the built library). */
 int ttk_abi_version(void);
@@ -200,6 +203,36 @@ ttk_status ttk_residual_layernorm_fwd(const void* x, const void* u,
  * 95-97), on the library GEMM's output.
  */
 ttk_status ttk_gelu_fwd(const void* x, void* y, int dtype, int64_t n, void* stream);
+
+/*
+ * Linear layer with an optional exact (erf) GELU, bf16 / fp16:
+ *
+ *   Y = act( round( X W^T + bias ) )
+ *
+ * X [M, K] (row stride ldx elements), W [N, K] (the nn.Linear weight, row
+ * stride ldw), bias [N] or NULL, Y [M, N] (row stride ldy), all of `dtype`.
+ * The product accumulates in fp32 and bias is added in fp32; the sum is
+ * rounded to dtype (round to nearest even), and with TTK_ACT_GELU the GELU of
+ * that rounded value is rounded again - the dtype boundaries of
+ * F.gelu(F.linear(x, W, b)) in 16-bit torch.  The bf16 GELU is exact: every
+ * result equals the correctly rounded x * Phi(x) of its input.
+ *
+ * Requirements (TTK_EUNSUPPORTED otherwise): dtype TTK_BF16 or TTK_F16; K a
+ * multiple of 128 and at least 256; N a multiple of 32; x, w and y 16-byte
+ * aligned, ldx, ldw and ldy multiples of 8 with ldx, ldw >= K and ldy >= N;
+ * bias 4-byte aligned; ((M - 1) * ldx + K) * 2 and ((N - 1) * ldw + K) * 2
+ * below 2^32 and M * ldy * 2 below 2^31.  y must not overlap x, w or bias
+ * (TTK_EINVAL).  M == 0 is a no-op.
+ *
+ * Replaces the FFN input projection and its separate GELU pass,
+ * `F.gelu(layer.ffn_in(h))` (reference transformer_opt/submission.py:507;
+ * benchmarks/torch_transformer_benchmark.py:95-97; the fused Linear + GELU
+ * candidate of benchmarks/experiments/c15_components.py:131-166), with the
+ * GELU applied in the GEMM's epilogue.
+ */
+ttk_status ttk_linear_fwd(const void* x, const void* w, const void* bias, void* y, int dtype,
+                          int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                          int64_t ldy, int activation, void* stream);
 
 #ifdef __cplusplus
 }

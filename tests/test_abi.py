@@ -166,3 +166,37 @@ def test_gelu_argument_errors_are_reported_without_launching():
     assert "overlap" in _native.last_error()
     assert f(1024 + 16, 1024, _native.TTK_F32, 8, None) == _native.TTK_EINVAL  # 32 bytes, 16 apart
     assert f(16, 16, _native.TTK_F32, 0, None) == _native.TTK_OK
+
+
+def _linear(lib, **over):
+    args = dict(x=1024, w=2048, b=None, y=4096, dtype=_native.TTK_BF16, M=64, N=256, K=256,
+                ldx=256, ldw=256, ldy=256, act=_native.TTK_ACT_GELU, stream=None)
+    args.update(over)
+    return lib.ttk_linear_fwd(args["x"], args["w"], args["b"], args["y"], args["dtype"], args["M"],
+                              args["N"], args["K"], args["ldx"], args["ldw"], args["ldy"], args["act"],
+                              args["stream"])
+
+
+def test_linear_argument_errors_are_reported_without_launching():
+    # Pointers here are fake: every call below is rejected before any HIP call.
+    lib = _native.load()
+    assert _linear(lib, dtype=_native.TTK_F32) == _native.TTK_EUNSUPPORTED
+    assert "not bf16 or fp16" in _native.last_error()
+    assert _linear(lib, act=7) == _native.TTK_EINVAL
+    assert _linear(lib, N=0) == _native.TTK_EINVAL
+    assert _linear(lib, K=200, ldx=200, ldw=200) == _native.TTK_EUNSUPPORTED
+    assert "multiple of 128" in _native.last_error()
+    assert _linear(lib, K=128, ldx=128, ldw=128) == _native.TTK_EUNSUPPORTED
+    assert _linear(lib, N=250, ldy=256) == _native.TTK_EUNSUPPORTED
+    assert "multiple of 32" in _native.last_error()
+    assert _linear(lib, x=1032) == _native.TTK_EUNSUPPORTED
+    assert "16-byte aligned" in _native.last_error()
+    assert _linear(lib, ldy=100) == _native.TTK_EUNSUPPORTED
+    assert _linear(lib, b=2050) == _native.TTK_EUNSUPPORTED
+    assert "4-byte aligned" in _native.last_error()
+    assert _linear(lib, M=1 << 22, N=1024, ldy=1024) == _native.TTK_EUNSUPPORTED
+    assert "2^31" in _native.last_error()
+    assert _linear(lib, y=1024 + 512) == _native.TTK_EINVAL  # y inside x
+    assert "overlaps" in _native.last_error()
+    assert _linear(lib, x=None) == _native.TTK_EINVAL
+    assert _linear(lib, M=0) == _native.TTK_OK  # nothing to launch

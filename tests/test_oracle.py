@@ -12,6 +12,7 @@ caught by at least one of these pins.
 
 from __future__ import annotations
 
+import math
 from pathlib import Path
 
 import numpy as np
@@ -34,6 +35,8 @@ from oracle.model import (
     copy_model_weights,
     generate_random_case,
 )
+
+REPO = Path(__file__).resolve().parent.parent
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "golden_v1.npz"
 
@@ -549,3 +552,44 @@ def test_planted_rounding_mistakes_are_caught_by_the_brute_force(mistake):
         got = np.nan_to_num(mistake(q, k, v, mask, causal, scale).numpy(), nan=1e9)
         worst = max(worst, float(np.abs(got - want).max()))
     assert worst > 1e-6
+
+
+def _bf16_value(bits: int) -> float:
+    return float(np.array([bits << 16], dtype=np.uint32).view(np.float32)[0])
+
+
+def test_gelu_bf16_table_is_the_correctly_rounded_exact_gelu():
+    # The fused Linear + GELU kernel's table (csrc/gelu_bf16_table.h) against
+    # an independent evaluation: torch's float64 erfc (not the generator's
+    # math.erfc), rounded to bf16 straight from float64 with numpy's
+    # round-half-even, for every entry; plus the rules the kernels rely on
+    # outside the table (identity for x >= 4, x/2 below 2^-16).
+    import re as _re
+
+    header = (REPO / "triton-transformer-kernels_amd" / "csrc" / "gelu_bf16_table.h").read_text()
+    first = int(_re.search(r"kGeluBf16First = (0x[0-9a-f]+)", header).group(1), 16)
+    per_sign = int(_re.search(r"kGeluBf16Pos = (\d+)", header).group(1))
+    body = header[header.index("= {") + 3:header.index("};")]
+    table = [int(v, 16) for v in _re.findall(r"0x[0-9a-f]{4}", body)]
+    assert len(table) == 2 * per_sign
+    bits = np.array([first + i for i in range(per_sign)] + [0x8000 | (first + i) for i in range(per_sign)])
+    x = torch.tensor([_bf16_value(int(b)) for b in bits], dtype=torch.float64)
+    exact = (x * 0.5 * torch.special.erfc(-x / math.sqrt(2.0))).numpy()
+    m, e = np.frexp(exact)
+    rounded = np.ldexp(np.rint(np.ldexp(m, 8)), e - 8)
+    got = np.array([_bf16_value(v) for v in table])
+    assert np.array_equal(got, rounded)
+    # Outside the table: GELU rounds to x itself for 4 <= x < 2^128 and to x/2
+    # for 2^-16 > |x| >= 2^-125 (bf16 normals), at bf16 precision.
+    outside = [b for b in range(0x0080, 0x7f80) if not first <= b < first + per_sign]
+    xs = torch.tensor([_bf16_value(b) for b in outside], dtype=torch.float64)
+    xs = torch.cat([xs, -xs[xs < 2.0 ** -16]])
+    gl = (xs * 0.5 * torch.special.erfc(-xs / math.sqrt(2.0))).numpy()
+    m, e = np.frexp(gl)
+    gl_r = np.ldexp(np.rint(np.ldexp(m, 8)), e - 8)
+    xv = xs.numpy()
+    big = xv >= 4
+    small = np.abs(xv) < 2.0 ** -16
+    assert np.array_equal(gl_r[big], xv[big])
+    normal_half = small & (np.abs(xv) >= 2.0 ** -125)
+    assert np.array_equal(gl_r[normal_half], xv[normal_half] / 2)

@@ -359,3 +359,75 @@ extern "C" ttk_status ttk_gelu_fwd(const void* x, void* y, int dtype, int64_t n,
   if (err != hipSuccess) return fail(TTK_ELAUNCH, "gelu: launch failed: %s", hipGetErrorString(err));
   return TTK_OK;
 }
+
+namespace {
+
+bool overlaps(const void* a, uint64_t abytes, const void* b, uint64_t bbytes) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + bbytes && y < x + abytes;
+}
+
+}  // namespace
+
+extern "C" ttk_status ttk_linear_fwd(const void* x, const void* w, const void* bias, void* y, int dtype,
+                                     int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                                     int64_t ldy, int activation, void* stream) {
+  g_error[0] = '\0';
+  if (dtype != TTK_BF16 && dtype != TTK_F16) {
+    return fail(TTK_EUNSUPPORTED, "linear: dtype code %d is not bf16 or fp16", dtype);
+  }
+  if (activation != TTK_ACT_NONE && activation != TTK_ACT_GELU) {
+    return fail(TTK_EINVAL, "linear: unknown activation code %d", activation);
+  }
+  if (M < 0 || N <= 0 || K <= 0) {
+    return fail(TTK_EINVAL, "linear: M must be >= 0 and N, K positive (M=%lld N=%lld K=%lld)",
+                (long long)M, (long long)N, (long long)K);
+  }
+  if (M == 0) return TTK_OK;
+  if (!x || !w || !y) return fail(TTK_EINVAL, "linear: x, w and y must not be NULL");
+  if (K % 128 != 0 || K < 256) {
+    return fail(TTK_EUNSUPPORTED, "linear: K=%lld must be a multiple of 128 and at least 256",
+                (long long)K);
+  }
+  if (N % 32 != 0) return fail(TTK_EUNSUPPORTED, "linear: N=%lld must be a multiple of 32", (long long)N);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y)) {
+    return fail(TTK_EUNSUPPORTED, "linear: x, w and y must be 16-byte aligned");
+  }
+  if (ldx % 8 != 0 || ldw % 8 != 0 || ldy % 8 != 0 || ldx < K || ldw < K || ldy < N) {
+    return fail(TTK_EUNSUPPORTED,
+                "linear: row strides must be multiples of 8 elements with ldx, ldw >= K and "
+                "ldy >= N (ldx=%lld ldw=%lld ldy=%lld)",
+                (long long)ldx, (long long)ldw, (long long)ldy);
+  }
+  if (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 3u) != 0) {
+    return fail(TTK_EUNSUPPORTED, "linear: bias must be 4-byte aligned");
+  }
+  const uint64_t xbytes = (static_cast<uint64_t>(M - 1) * ldx + K) * 2;
+  const uint64_t wbytes = (static_cast<uint64_t>(N - 1) * ldw + K) * 2;
+  const uint64_t ybytes = static_cast<uint64_t>(M) * ldy * 2;
+  if (xbytes >= (uint64_t{1} << 32) || wbytes >= (uint64_t{1} << 32) || ybytes >= (uint64_t{1} << 31)) {
+    return fail(TTK_EUNSUPPORTED,
+                "linear: x or w spans 2^32 bytes or more, or y 2^31 bytes or more (M=%lld N=%lld "
+                "K=%lld)",
+                (long long)M, (long long)N, (long long)K);
+  }
+  if (overlaps(y, ybytes, x, xbytes) || overlaps(y, ybytes, w, wbytes) ||
+      (bias != nullptr && overlaps(y, ybytes, bias, static_cast<uint64_t>(N) * 2))) {
+    return fail(TTK_EINVAL, "linear: y overlaps x, w or bias");
+  }
+  ttk::LinearParams p{};
+  p.x = x;
+  p.w = w;
+  p.bias = bias;
+  p.y = y;
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldy = ldy;
+  p.M = static_cast<int>(M);
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.y_bytes = static_cast<unsigned>(ybytes);
+  const hipError_t err = ttk::launch_linear(dtype, activation, p, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(TTK_ELAUNCH, "linear: launch failed: %s", hipGetErrorString(err));
+  return TTK_OK;
+}

@@ -134,6 +134,21 @@ struct LnParams {
   int zero_norm;
 };
 
+// Launch parameters of the Linear (+ activation) kernel: Y = act(X W^T + b),
+// X [M, K], W [N, K], Y [M, N] row-major with element leading dimensions.
+struct LinearParams {
+  const void* x;
+  const void* w;
+  const void* bias;  // [N] or null
+  void* y;
+  int64_t ldx, ldw, ldy;
+  int M, N, K;
+  int tiles_m, tiles_n, tiles;
+  int per_xcd;       // tiles dealt to each XCD (the last may get fewer)
+  int group_m;       // token tiles per band of the tile order
+  unsigned y_bytes;  // bytes of Y addressed by the store resource
+};
+
 // Host-side launchers (defined next to their kernels).  Return a HIP error.
 // launch_attention fills p.pair / p.units / the split plan and sizes the
 // grid itself.  `workspace` (workspace_bytes, 256-byte aligned) may be null;
@@ -151,5 +166,9 @@ hipError_t launch_residual_layernorm(int dtype, const LnParams& p, bool vector_p
 
 // Exact GELU over n contiguous elements of dtype (0 fp32, 1 bf16, 2 fp16).
 hipError_t launch_gelu(int dtype, const void* x, void* y, int64_t n, hipStream_t stream);
+
+// Linear + activation (0 none, 1 exact GELU) for dtype 1 (bf16) or 2 (fp16);
+// fills the tile fields of p and sizes the grid.
+hipError_t launch_linear(int dtype, int activation, LinearParams& p, hipStream_t stream);
 
 }  // namespace ttk

@@ -25,6 +25,9 @@ TTK_F32 = 0
 TTK_BF16 = 1
 TTK_F16 = 2
 
+TTK_ACT_NONE = 0
+TTK_ACT_GELU = 1
+
 # Exported symbols (kept in the same order as include/ttk_hip.h).
 EXPORTED_SYMBOLS = (
     "ttk_abi_version",
@@ -35,8 +38,9 @@ EXPORTED_SYMBOLS = (
     "ttk_attention_fwd_noalloc",
     "ttk_residual_layernorm_fwd",
     "ttk_gelu_fwd",
+    "ttk_linear_fwd",
 )
-ABI_VERSION = 7
+ABI_VERSION = 8
 # TTK_ATTENTION_WS_COUNTER_BYTES: the zero-initialised counter block that
 # leads every attention workspace, the same for every launch shape.
 ATTENTION_WS_COUNTER_BYTES = 16384
@@ -85,6 +89,9 @@ def _configure(lib: ctypes.CDLL) -> None:
     ]
     lib.ttk_gelu_fwd.restype = ctypes.c_int
     lib.ttk_gelu_fwd.argtypes = [_vp, _vp, ctypes.c_int, _i64, _vp]
+    lib.ttk_linear_fwd.restype = ctypes.c_int
+    lib.ttk_linear_fwd.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i64, _i64, _i64, _i64,
+                                   _i64, ctypes.c_int, _vp]
 
 
 def load() -> ctypes.CDLL:

@@ -2,6 +2,7 @@
 
 from .attention import hip_attention, hip_available, triton_attention, triton_available
 from .gelu import gelu, gelu_
+from .linear import linear, linear_gelu, linear_supported
 from .residual_layer_norm import fused_residual_layer_norm, layer_norm, short_layer_norm
 
 __all__ = [
@@ -11,6 +12,9 @@ __all__ = [
     "hip_attention",
     "hip_available",
     "layer_norm",
+    "linear",
+    "linear_gelu",
+    "linear_supported",
     "short_layer_norm",
     "triton_attention",
     "triton_available",

@@ -37,9 +37,10 @@ the dispatcher (never chosen otherwise) and counts it there; the packed QKV
 projection is used for every width and dtype (submission.py:184-190
 restricted it); graph replay is eligible for every supported shape and dtype
 instead of a measured shape set (submission.py:582-590), with up to
-``max_cuda_graphs`` captures kept, one per input geometry.  Projections and
-the FFN are library GEMMs (hipBLASLt through ``F.linear``); the FFN's exact
-GELU runs in place on the HIP elementwise kernel.  The model is
+``max_cuda_graphs`` captures kept, one per input geometry.  Projections are
+library GEMMs (hipBLASLt through ``F.linear``); in bf16 the FFN's input
+projection and exact GELU are one HIP kernel (GELU in the GEMM epilogue),
+otherwise the GELU runs in place on the HIP elementwise kernel.  The model is
 forward-inference only: with gradients enabled on parameters that require
 them the kernels raise, as there is no backward kernel.
 """
@@ -55,6 +56,7 @@ import torch.nn.functional as F
 from .config import ATTENTION_BACKENDS, SUPPORTED_DTYPES
 from .dispatch import attention_forward
 from .kernels.gelu import gelu_
+from .kernels.linear import linear_gelu, linear_supported
 from .kernels.residual_layer_norm import fused_residual_layer_norm, layer_norm
 from .model import TransformerBlock, TransformerConfig
 from .replay import CapturedForward, ReplayCache
@@ -329,7 +331,19 @@ class UserOptimizedTransformer(nn.Module):
 
     @staticmethod
     def _feed_forward(block: _Block, h: torch.Tensor) -> torch.Tensor:
-        inner = gelu_(F.linear(h, block.ffn_in_weight, block.ffn_in_bias))
+        """FFN: ``ffn_out(gelu(ffn_in(h)))`` (reference submission.py:506-508).
+
+        bf16: the input projection and its exact GELU are one HIP kernel, the
+        GELU in the GEMM's epilogue (same dtype boundaries: the projection is
+        rounded to bf16, its GELU rounded again).  Otherwise, and for widths
+        that kernel does not take, the library GEMM writes the projection and
+        the HIP elementwise GELU runs in place on it.
+        """
+        w, b = block.ffn_in_weight, block.ffn_in_bias
+        if h.dtype == torch.bfloat16 and linear_supported(h, w, b) is None:
+            inner = linear_gelu(h, w, b)
+        else:
+            inner = gelu_(F.linear(h, w, b))
         return F.linear(inner, block.ffn_out_weight, block.ffn_out_bias)
 
     @staticmethod
