@@ -195,6 +195,7 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
   constexpr int KS = kLinBK / 16;           // k-steps per stage
   constexpr int MF = 4 * TJ;                // MFMAs per k-step
   constexpr int kGap = MF / HALF;           // MFMAs per copy
+  constexpr int STORES = 8 * TJ;            // stores per wavefront per tile
   static_assert(kGap >= 1 && MF % HALF == 0, "copies spread evenly over a k-step");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -275,9 +276,11 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
   // One k-step: MF MFMAs on (wf, xf).  In their shadow go the fragment reads
   // of the next k-step (one after each of the first 4 + TJ MFMAs) and, when
   // d.on, copies HALF * half .. + HALF - 1 of stage d.ks of the tile at
-  // (d.m0, d.n0) into ring buffer d.buf, one every kGap MFMAs.
+  // (d.m0, d.n0) into ring buffer d.buf, one every kGap MFMAs - or, with
+  // `both`, all DMA copies of the stage, evenly spread.
   auto kstep = [&](auto zero, const u16x8 (&wf)[4], const u16x8 (&xf)[TJ], int rbuf, int rkk,
-                   u16x8 (&nw)[4], u16x8 (&nx)[TJ], const Pending& d, int half) __attribute__((always_inline)) {
+                   u16x8 (&nw)[4], u16x8 (&nx)[TJ], const Pending& d, int half,
+                   auto both) __attribute__((always_inline)) {
     const unsigned char* wb = wfrag[rkk] + rbuf * kLinOpBytes;
     const unsigned char* xb = xfrag[rkk] + rbuf * kLinOpBytes;
 #pragma unroll
@@ -290,7 +293,13 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
       }
       if (t < 4) nw[t] = *reinterpret_cast<const u16x8*>(wb + 32 * (kLinBK * 2) * t);
       else if (t < 4 + TJ) nx[t - 4] = *reinterpret_cast<const u16x8*>(xb + 32 * (kLinBK * 2) * (t - 4));
-      if (t % kGap == (kGap > 1 ? 1 : 0) && d.on) issue_one(d.m0, d.n0, d.ks, d.buf, HALF * half + t / kGap);
+      if constexpr (decltype(both)::value) {
+        constexpr int kGap2 = MF / DMA;
+        static_assert(kGap2 >= 1 && MF % DMA == 0, "all copies fit one k-step");
+        if (t % kGap2 == 0 && d.on) issue_one(d.m0, d.n0, d.ks, d.buf, t / kGap2);
+      } else if (t % kGap == (kGap > 1 ? 1 : 0) && d.on) {
+        issue_one(d.m0, d.n0, d.ks, d.buf, HALF * half + t / kGap);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -392,10 +401,11 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
               ? static_cast<unsigned>(m) * y_pitch + static_cast<unsigned>(f) * 2u
               : 0x80000000u;
           __builtin_amdgcn_raw_buffer_store_b128(v, yrsrc, static_cast<int>(off), 0, 0);
-          // One group of 8 outputs at a time: unfenced, the scheduler hoists
-          // the table reads of many groups and runs out of registers.
-          __builtin_amdgcn_sched_barrier(0);
         }
+        // Two groups of 8 outputs at a time (the table reads of one overlap
+        // the other's arithmetic); unfenced, the scheduler hoists the table
+        // reads of many groups and runs out of registers.
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
@@ -407,10 +417,14 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
   // free, and stage s + 1 must be in LDS.  Stage s + 2's copies go into that
   // buffer in two halves, in the last k-step of s and the first of s + 1;
   // at stage s's barrier the only copies outstanding are stage s + 1's, so
-  // the wait is vmcnt(0).  Stages run in pairs (one per buffer): the first
-  // pair of a tile (accumulators start at zero), the middle pairs and the
-  // last pair (copies of the next tile's first stages, if any); NS >= 4
-  // keeps the first and last apart.
+  // the wait is vmcnt(0).  The exception is the tile boundary: the last
+  // k-step of a tile issues all of the next tile's stage-1 copies, so that
+  // the epilogue's STORES stores come after every copy the next tile's first
+  // barrier waits for, and that barrier waits vmcnt(STORES) - the stores
+  // drain while the next tile computes.  Stages run in pairs (one per
+  // buffer): the first pair of a tile (accumulators start at zero), the
+  // middle pairs and the last pair (copies of the next tile's first stages,
+  // if any); NS >= 4 keeps the first and last apart.
   const int NS = p.K / kLinBK;
   bool has_next = find_next();
 #pragma unroll
@@ -432,6 +446,7 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
   constexpr std::integral_constant<int, 2> kLast{};
   Pending pend{false, 0, 0, 0, 0};  // second half of the copies last issued
   const Pending none{false, 0, 0, 0, 0};
+  bool first = true;
   for (;;) {
     auto pair = [&](auto kind, int s0) __attribute__((always_inline)) {
       constexpr int K = decltype(kind)::value;
@@ -441,9 +456,9 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
         for (int kk = 0; kk + 1 < KS; ++kk) {
           const int a = kk & 1;
           if (K == 0 && u == 0 && kk == 0) {
-            kstep(kYes, fw[a], fx[a], u, kk + 1, fw[a ^ 1], fx[a ^ 1], pend, 1);
+            kstep(kYes, fw[a], fx[a], u, kk + 1, fw[a ^ 1], fx[a ^ 1], none, 1, kNo);
           } else {
-            kstep(kNo, fw[a], fx[a], u, kk + 1, fw[a ^ 1], fx[a ^ 1], kk == 0 ? pend : none, 1);
+            kstep(kNo, fw[a], fx[a], u, kk + 1, fw[a ^ 1], fx[a ^ 1], kk == 0 ? pend : none, 1, kNo);
           }
         }
         // Last k-step: the barrier, then stage s + 2's first copies.
@@ -456,11 +471,19 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
           }
           pend = Pending{has_next, nm, nn, u, u};
         } else {
-          lin_vm_wait(0);
+          // The first stage of a tile after the first: the previous tile's
+          // stores came after all of stage 1's copies.
+          lin_vm_wait((K == 0 && u == 0 && !first) ? STORES : 0);
           __syncthreads();
           pend = Pending{true, cm, cn, s0 + u + 2, u};
         }
-        kstep(kNo, fw[a], fx[a], u ^ 1, 0, fw[a ^ 1], fx[a ^ 1], pend, 0);
+        if (K == 2 && u == 1) {
+          // The next tile's stage 1, all copies before the epilogue.
+          kstep(kNo, fw[a], fx[a], u ^ 1, 0, fw[a ^ 1], fx[a ^ 1], pend, 0, kYes);
+          pend = none;
+        } else {
+          kstep(kNo, fw[a], fx[a], u ^ 1, 0, fw[a ^ 1], fx[a ^ 1], pend, 0, kNo);
+        }
       }
     };
     pair(kFirst, 0);
@@ -471,6 +494,7 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
     cm = nm;
     cn = nn;
     has_next = find_next();
+    first = false;
   }
 }
 
