@@ -24,8 +24,10 @@ Also reported in the same line:
   clock ramp;
 * ``secondary``: the S sweep {256..4096} causal/non-causal (config 2), the
   residual+LayerNorm HBM GB/s per hidden size with rotating input sets larger
-  than the 256 MB MALL (config 3), bf16 long-sequence attention (config 5a)
-  and encoder tokens/s with hipGraph replay (config 4, fp32 and bf16).  Each
+  than the 256 MB MALL (config 3), bf16 long-sequence attention (config 5a),
+  the config-4 FFN input in bf16 as the fused Linear + exact-GELU kernel
+  against the library GEMM plus the GELU kernel, and encoder tokens/s with
+  hipGraph replay (config 4, fp32 and bf16).  Each
   figure there follows 1 s of untimed calls of its own workload (the clock
   follows the power draw of the work in flight), and each kernel figure is
   the average launch over back-to-back launches between two events, as for
@@ -139,6 +141,44 @@ def back_to_back_ms(fn, steps: int, warmup: int, settle_s: float = SECONDARY_SET
     finish.record(stream)
     torch.cuda.synchronize()
     return begin.elapsed_time(finish) / steps
+
+
+def ffn_input_operands():
+    """The config-4 encoder's FFN input projection in bf16: activations
+    [8192, 1024] ~ N(0, 1), Xavier-uniform weight [4096, 1024], bias ~ N(0, 0.02)."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(8192, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    bound = (6.0 / (1024 + 4096)) ** 0.5
+    w = ((torch.rand(4096, 1024, device="cuda", generator=g) * 2 - 1) * bound).to(torch.bfloat16)
+    b = (torch.randn(4096, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    return x, w, b
+
+
+def ffn_input_ab(steps: int = 50, warmup: int = 10) -> dict:
+    """Per-call times (us) of the config-4 FFN input in bf16: the fused Linear +
+    exact-GELU kernel against what it replaces (library GEMM, then the
+    elementwise GELU kernel in place), alternating twice, best of each."""
+    import torch
+    import torch.nn.functional as F
+
+    from transformer_opt.kernels import gelu_, linear_gelu
+
+    x, w, b = ffn_input_operands()
+    routes = {"fused_linear_gelu": lambda: linear_gelu(x, w, b),
+              "library_gemm_then_gelu": lambda: gelu_(F.linear(x, w, b)),
+              "library_gemm_only": lambda: F.linear(x, w, b)}
+    best = {}
+    with torch.inference_mode():
+        for _ in range(2):
+            for name, fn in routes.items():
+                us = back_to_back_ms(fn, steps, warmup) * 1e3
+                best[name] = min(best.get(name, us), us)
+    flop = 2.0 * 8192 * 4096 * 1024
+    out = {name: {"us": round(us, 2), "tflops": round(flop / us / 1e6, 1)} for name, us in best.items()}
+    out["fused_speedup_vs_pair"] = round(best["library_gemm_then_gelu"] / best["fused_linear_gelu"], 3)
+    return out
 
 
 def attention_tflops(batch, seq_len, heads, head_dim, causal, dtype, steps=10, warmup=3):
@@ -345,6 +385,10 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
     encoder_5b:     config-5b encoder forward (fp32, B=512, S=64, d=512, 4 layers,
                     hipGraph replay), for the per-kernel split
     gelu:           exact GELU, bf16, the config-4 FFN activation [8192, 4096] (GB/s)
+    linear_gelu:    fused Linear + exact GELU, bf16, the config-4 FFN input
+                    ([8192, 1024] x [4096, 1024]^T + b)
+    linear_gelu_pair: the same FFN input as the library GEMM (F.linear) followed by
+                    the elementwise GELU kernel in place (what the fused kernel replaces)
     layernorm:      fp32 residual+LN rows=32768, hidden = --hidden (config 3), rotating
                     among input sets that together exceed twice the 256 MB MALL
     layernorm_bf16: bf16 residual+LN rows=8192, hidden=1024 (the config-4 encoder's LN),
@@ -412,6 +456,15 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         act = torch.randn(8192, 4096, device="cuda").to(torch.bfloat16)
         fn = lambda: gelu_(act)  # noqa: E731
         work = 2.0 * act.numel() * 2  # bytes: read and write once
+    elif which in ("linear_gelu", "linear_gelu_pair"):
+        from transformer_opt.kernels import gelu_, linear_gelu
+
+        x, w, b = ffn_input_operands()
+        if which == "linear_gelu":
+            fn = lambda: linear_gelu(x, w, b)  # noqa: E731
+        else:
+            fn = lambda: gelu_(torch.nn.functional.linear(x, w, b))  # noqa: E731
+        work = 2.0 * 8192 * 4096 * 1024
     elif which in ("encoder_fp32", "encoder_bf16"):
         from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
 
@@ -486,7 +539,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "layernorm_bf16", "copy", "attention_bf16",
                                                    "attention_bf16_d64", "attention_5b", "encoder_fp32", "encoder_bf16",
-                                                   "encoder_5b", "gelu"),
+                                                   "encoder_5b", "gelu", "linear_gelu", "linear_gelu_pair"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")
@@ -659,6 +712,10 @@ def main() -> int:
             small[f"D{d_head}_{name}"] = {"tflops": round(tf, 2), "ms": round(ms, 4)}
             log(f"attention {name} causal [8,1024,16,{d_head}]: {tf:.1f} TF")
         secondary["attention_small_head_dim_causal_B8_S1024_H16"] = small
+        torch.cuda.empty_cache()
+        ffn = ffn_input_ab()
+        secondary["ffn_input_bf16_8192x4096x1024"] = ffn
+        log(f"FFN input bf16: {ffn}")
         torch.cuda.empty_cache()
         model = {}
         for dtype_name in ("fp32", "bf16"):
