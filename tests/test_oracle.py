@@ -572,7 +572,16 @@ def test_gelu_bf16_table_is_the_correctly_rounded_exact_gelu():
     body = header[header.index("= {") + 3:header.index("};")]
     table = [int(v, 16) for v in _re.findall(r"0x[0-9a-f]{4}", body)]
     assert len(table) == 2 * per_sign
-    bits = np.array([first + i for i in range(per_sign)] + [0x8000 | (first + i) for i in range(per_sign)])
+    # Entry 2u + s: sign bit s, magnitude bits first + u.
+    bits = np.array([((i & 1) << 15) | (first + (i >> 1)) for i in range(2 * per_sign)])
+    # The kernel's index: the 16-bit input rotated left by one (sign to bit 0)
+    # minus 2 * first, modulo 2^16 - below 2 * per_sign exactly for the inputs
+    # the table holds, and then their entry.
+    every = np.arange(65536, dtype=np.int64)
+    index = (((every << 1) | (every >> 15)) - 2 * first) & 0xFFFF
+    held = ((every & 0x7FFF) >= first) & ((every & 0x7FFF) < first + per_sign)
+    assert np.array_equal(index < 2 * per_sign, held)
+    assert np.array_equal(bits[index[held]], every[held])
     x = torch.tensor([_bf16_value(int(b)) for b in bits], dtype=torch.float64)
     exact = (x * 0.5 * torch.special.erfc(-x / math.sqrt(2.0))).numpy()
     m, e = np.frexp(exact)

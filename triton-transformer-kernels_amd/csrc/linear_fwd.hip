@@ -14,10 +14,10 @@
 // The GELU of a bf16 value is read from a table of the exact GELU of every
 // bf16 input in (-8, -2^-16] and [2^-16, 8), correctly rounded
 // (gelu_bf16_table.h, generated in float64), kept in LDS: per pair of
-// outputs a handful of packed 16-bit integer operations and two LDS reads
-// replace the ~17 VALU operations per element of an erf evaluation.  Inputs
-// outside the table (rare: GELU is x there, or x/2 at bf16 precision) take
-// gelu_exact().  fp16 evaluates gelu_exact() on every element.
+// outputs five packed 16-bit integer operations, two LDS reads and a byte
+// permute replace the ~17 VALU operations per element of an erf evaluation.
+// Inputs outside the table (rare: GELU is x there, or x/2 at bf16 precision)
+// take gelu_exact().  fp16 evaluates gelu_exact() on every element.
 //
 // Design (one workgroup = 4 wavefronts, one per SIMD; a 256 x 256 tile):
 // * The MFMA computes the transposed tile C^T[n, m] = W . X^T with
@@ -25,15 +25,18 @@
 //   row, and in the result a lane holds one token and 4 consecutive features
 //   per register group.  Each wavefront owns 128 features x 128 tokens:
 //   4 x 4 MFMA tiles, 256 fp32 accumulators (AGPRs).
-// * K advances in stages of 32 through a 4-deep LDS ring per operand
-//   (4 x 16 KB).  Stages are copied global -> LDS by LDS-DMA; the copy of
-//   stage s + 4 is issued right after the barrier that retires stage s, so a
-//   copy has three and a half stages of compute to land.  Rows are 64 bytes
-//   of four 16-byte chunks, chunk c of row r stored at c ^ ((r >> 2) & 3):
-//   the 16-byte operand reads of 16 consecutive rows then cover all 64 banks.
+// * K advances in stages of 64 through a 2-deep LDS ring per operand
+//   (2 x 32 KB), after the 9.5 KB GELU table: 137.5 KB of LDS, one
+//   workgroup per CU.  Stages are copied global -> LDS by LDS-DMA, spread
+//   over the MFMAs of the k-steps around the barrier that frees their buffer
+//   (one copy every 4 MFMAs), so a copy has about one stage of compute to
+//   land.  Rows are 128 bytes of eight 16-byte chunks, chunk c of row r
+//   stored at c ^ ((r >> 1) & 7): the 16-byte operand reads of 16
+//   consecutive rows then cover all 64 banks.
 // * Persistent grid: each workgroup walks its tiles, and the copies of the
-//   next tile's first stages are issued during the current tile's last
-//   stages, so they land while the epilogue runs.
+//   next tile's first two stages are issued during the current tile's last
+//   two, so they land while the epilogue runs and its stores drain while
+//   the next tile computes.
 // * Tile order: workgroups are dealt round-robin to the 8 XCDs, so the slots
 //   of one workgroup stay on one XCD; each XCD gets a contiguous band of the
 //   tile grid (group_m token tiles x all feature tiles), and the workgroups
@@ -96,22 +99,36 @@ __device__ __forceinline__ unsigned lpack(F16, float a, float b) {
   return __builtin_bit_cast(unsigned, v);
 }
 
-// Exact GELU of two packed bf16 values from the LDS table (`tab`): entry
-// u + 2432 * sign for magnitude bits u = |bits| - 0x3780 below 2432.  `ok`
-// reports whether both inputs were inside the table; the index is clamped, so
-// the reads stay inside it either way.
-__device__ __forceinline__ unsigned gelu_pair_table(unsigned pre, const unsigned short* tab, bool& ok) {
+// Table index of two packed bf16 values: each 16-bit half rotated left by one
+// (sign to bit 0) minus 2 * kGeluBf16First, i.e. 2 (magnitude - first) + sign
+// modulo 2^16 - below kGeluBf16Entries exactly for the inputs the table holds.
+// Three instructions: the sign bits, or-ed with -2 * first (0x9100), are the
+// addend of a packed multiply-add of the bits by 2 (whose product drops the
+// sign bit).
+__device__ __forceinline__ unsigned gelu_table_index(unsigned pre) {
+  static_assert(((0x10000 - 2 * kGeluBf16First) & 1) == 0, "the sign bit fits below the addend");
   const us2 bits = __builtin_bit_cast(us2, pre);
-  const us2 u = (bits & static_cast<unsigned short>(0x7fff)) - static_cast<unsigned short>(kGeluBf16First);
+  const us2 addend = (bits >> static_cast<unsigned short>(15)) |
+                     static_cast<unsigned short>(0x10000 - 2 * kGeluBf16First);
+  unsigned r;
+  asm("v_pk_mad_u16 %0, %1, 2, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(pre), "v"(__builtin_bit_cast(unsigned, addend)));
+  return r;
+}
+// Exact GELU of two packed bf16 values from the table at the start of the
+// kernel's LDS (`smem`), given their index pair r (gelu_table_index).  The index is clamped, so the
+// reads stay inside the table for any input.
+__device__ __forceinline__ unsigned gelu_pair_table(unsigned r, const unsigned char* smem) {
   const us2 last = {static_cast<unsigned short>(kGeluBf16Entries - 1),
                     static_cast<unsigned short>(kGeluBf16Entries - 1)};
-  const us2 idx = __builtin_elementwise_min(
-      u + (bits >> static_cast<unsigned short>(15)) * static_cast<unsigned short>(kGeluBf16Pos), last);
-  us2 out;
-  out.x = tab[idx.x];
-  out.y = tab[idx.y];
-  ok = (u.x < kGeluBf16Pos) & (u.y < kGeluBf16Pos);
-  return __builtin_bit_cast(unsigned, out);
+  const unsigned c = __builtin_bit_cast(unsigned, __builtin_elementwise_min(__builtin_bit_cast(us2, r), last));
+  unsigned lo_byte;  // 2 * low index: one multiply-add on the low half
+  asm("v_mad_u32_u16 %0, %1, 2, 0" : "=v"(lo_byte) : "v"(c));
+  const unsigned hi_byte = c >> 15;  // 2 * high index (the low index is below 2^15)
+  // Two 16-bit reads, merged by one byte permute (16-bit loads into register
+  // halves zero the other half on this GPU, so they cannot merge in place).
+  const unsigned lo = *reinterpret_cast<const unsigned short*>(smem + lo_byte);
+  const unsigned hi = *reinterpret_cast<const unsigned short*>(smem + hi_byte);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 // Exact GELU of two packed values by evaluation (inputs outside the table,
 // and fp16).
@@ -204,7 +221,6 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
   const int h = lane >> 5;
   const int wn = wave & 1;   // feature half of the tile (128 features)
   const int wm = wave >> 1;  // token block of the tile (WT tokens)
-  const unsigned short* tab = reinterpret_cast<const unsigned short*>(smem);
 
   // The slots of this workgroup: blockIdx.x, + gridDim.x, ... (one XCD).
   const int grid = static_cast<int>(gridDim.x);
@@ -341,6 +357,10 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
           bq[g][2] = to_f32(T{}, static_cast<unsigned short>(hi));
           bq[g][3] = to_f32(T{}, static_cast<unsigned short>(hi >> 16));
         }
+        // Materialised once per feature block (otherwise the compiler
+        // rebuilds them from the scalar registers for every token block).
+#pragma unroll
+        for (int g = 0; g < 4; ++g) asm volatile("" : "+v"(bq[g][0]), "+v"(bq[g][1]), "+v"(bq[g][2]), "+v"(bq[g][3]));
       }
 #pragma unroll
       for (int j = 0; j < TJ; ++j) {
@@ -357,18 +377,26 @@ __global__ __launch_bounds__(64 * NW, 1) void linear_kernel(LinearParams p) {
             for (int e = 0; e < 4; ++e) v[e] = BIAS ? acc[i][j][4 * g + e] + bq[g][e] : acc[i][j][4 * g + e];
             o[k][0] = lpack(T{}, v[0], v[1]);
             o[k][1] = lpack(T{}, v[2], v[3]);
+            // Opaque, so the compiler keeps the packed conversion (it would
+            // convert each half again to take the table index apart).
+            asm volatile("" : "+v"(o[k][0]), "+v"(o[k][1]));
           }
           if constexpr (kTable) {
             // Table reads for all eight; in the rare group where some lane
             // holds an input outside the table (a wave-uniform branch), every
             // lane evaluates and keeps the evaluation for those inputs only.
-            bool ok[2][2];
-            unsigned t[2][2];
+            unsigned r[2][2], t[2][2];
 #pragma unroll
             for (int k = 0; k < 2; ++k)
 #pragma unroll
-              for (int d = 0; d < 2; ++d) t[k][d] = gelu_pair_table(o[k][d], tab, ok[k][d]);
-            const bool all_ok = ok[0][0] & ok[0][1] & ok[1][0] & ok[1][1];
+              for (int d = 0; d < 2; ++d) {
+                r[k][d] = gelu_table_index(o[k][d]);
+                t[k][d] = gelu_pair_table(r[k][d], smem);
+              }
+            const us2 rmax = __builtin_elementwise_max(
+                __builtin_elementwise_max(__builtin_bit_cast(us2, r[0][0]), __builtin_bit_cast(us2, r[0][1])),
+                __builtin_elementwise_max(__builtin_bit_cast(us2, r[1][0]), __builtin_bit_cast(us2, r[1][1])));
+            const bool all_ok = (rmax.x < kGeluBf16Entries) & (rmax.y < kGeluBf16Entries);
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!all_ok) != 0, 0)) {
 #pragma unroll
               for (int k = 0; k < 2; ++k)
