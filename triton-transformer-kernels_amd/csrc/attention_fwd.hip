@@ -126,10 +126,12 @@ __device__ __forceinline__ float dot2_ones(F16, unsigned pair, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, 0x3C003C00u),
                                 acc, false);
 }
-template <typename T, int NP>
+// Row sum of the first NU packed registers (all by default).
+template <typename T, int NP, int NU = NP>
 __device__ __forceinline__ float add_packed(const u16x8 (&pn)[NP], float acc) {
+  static_assert(NU <= NP, "registers in use");
 #pragma unroll
-  for (int i = 0; i < NP; ++i) {
+  for (int i = 0; i < NU; ++i) {
     const u32x4 w = __builtin_bit_cast(u32x4, pn[i]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc = dot2_ones(T{}, w[j], acc);
@@ -268,16 +270,17 @@ __device__ __forceinline__ uint32_t lane_allowed(uint32_t sub_valid, int ks, int
   return a >> (4 * h);
 }
 
-// Sets scores of disallowed keys to -inf (tile of NSB sub-blocks from k0).
+// Sets scores of disallowed keys to -inf (tile of NSB sub-blocks from k0;
+// only the first NL are touched - the caller has not computed the others).
 // BITSEL: per register, a signed one-bit field extract of the allowed bit
 // gives an all-ones / all-zeros word and a bit-field insert selects the score
 // or -inf - two VALU instructions and no compare, so no VCC write that the
 // select has to wait for.  Otherwise a compare and a select per register
 // (fewer live registers where the kernel is at its register limit).
-template <int NSB, bool CAUSAL, bool BITSEL = true>
+template <int NSB, bool CAUSAL, bool BITSEL = true, int NL = NSB>
 __device__ __forceinline__ void apply_mask(f32x16 (&s)[NSB], int k0, uint64_t kvalid, int qrow, int h) {
 #pragma unroll
-  for (int sb = 0; sb < NSB; ++sb) {
+  for (int sb = 0; sb < NL; ++sb) {
     const uint32_t a =
         lane_allowed<CAUSAL>(static_cast<uint32_t>(kvalid >> (32 * sb)), k0 + sb * 32, qrow, h);
 #pragma unroll
@@ -1411,48 +1414,61 @@ __global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWave
     // S^T = K(buf) . Q^T.  K fragments run PDK groups ahead in a ring: the
     // slot of group g is refilled with group g + PDK right after group g's
     // MFMAs issue, so an LDS read has PDK - 1 groups of MFMAs to land.
-    auto qk = [&](auto masked_tag, int buf, int nlive, f32x16 (&s)[NSB]) {
-      constexpr bool MASKED = decltype(masked_tag)::value;
+    // Only the first L sub-blocks (a compile-time count: the live ones of a
+    // masked tile) are computed; the others are left untouched.  A run-time
+    // count would put every MFMA of sub-block 1 under its own branch, and the
+    // compiler then copies its 16 accumulators through every branch.
+    auto qk = [&](auto live_tag, int buf, f32x16 (&s)[NSB]) {
+      constexpr int L = decltype(live_tag)::value;
+      static_assert(L >= 1 && L <= NSB, "live sub-blocks");
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
+      for (int sb = 0; sb < L; ++sb) s[sb] = f32x16{};
       u16x8 kr[PDK][NSB];
 #pragma unroll
       for (int i = 0; i < PDK && i < G; ++i)
 #pragma unroll
-        for (int sb = 0; sb < NSB; ++sb)
-          if (!MASKED || sb < nlive) kr[i][sb] = kread(buf, sb, i);
+        for (int sb = 0; sb < L; ++sb) kr[i][sb] = kread(buf, sb, i);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
 #pragma unroll
-        for (int sb = 0; sb < NSB; ++sb) {
-          if (MASKED && sb >= nlive) continue;
-          s[sb] = mfma_16(T{}, kr[g % PDK][sb], qf[g], s[sb]);
-        }
+        for (int sb = 0; sb < L; ++sb) s[sb] = mfma_16(T{}, kr[g % PDK][sb], qf[g], s[sb]);
         if (g + PDK < G) {
 #pragma unroll
-          for (int sb = 0; sb < NSB; ++sb)
-            if (!MASKED || sb < nlive) kr[g % PDK][sb] = kread(buf, sb, g + PDK);
+          for (int sb = 0; sb < L; ++sb) kr[g % PDK][sb] = kread(buf, sb, g + PDK);
         }
         fence();
       }
     };
 
-    // O^T += V^T(buf) . P^T; V fragments run PDV steps ahead in a ring.
-    auto pv = [&](int buf, int nlive) __attribute__((always_inline)) {
-      const int nsteps = nlive * 2 * NDB;
+    // O^T += V^T(buf) . P^T over the first L sub-blocks (compile-time, as in
+    // qk); V fragments run PDV steps ahead in a ring.
+    auto pv = [&](int buf, auto live_tag) __attribute__((always_inline)) {
+      constexpr int L = decltype(live_tag)::value;
+      constexpr int nsteps = L * 2 * NDB;
       u16x8 vr[PDV];
 #pragma unroll
-      for (int i = 0; i < PDV && i < NSTEP; ++i)
-        if (i < nsteps) vr[i] = vread(buf, i);
+      for (int i = 0; i < PDV && i < nsteps; ++i) vr[i] = vread(buf, i);
 #pragma unroll
-      for (int idx = 0; idx < NSTEP; ++idx) {
-        if (idx < nsteps) {
-          acc[idx % NDB] = mfma_16(T{}, vr[idx % PDV], pk[idx / NDB], acc[idx % NDB]);
-          if (idx + PDV < NSTEP && idx + PDV < nsteps) vr[idx % PDV] = vread(buf, idx + PDV);
-        }
+      for (int idx = 0; idx < nsteps; ++idx) {
+        acc[idx % NDB] = mfma_16(T{}, vr[idx % PDV], pk[idx / NDB], acc[idx % NDB]);
+        if (idx + PDV < nsteps) vr[idx % PDV] = vread(buf, idx + PDV);
         fence();
       }
     };
+    // Calls f with the live sub-block count n (1 .. NSB) as a compile-time
+    // constant.
+    auto with_live = [&](int n, auto&& f) __attribute__((always_inline)) {
+      if constexpr (NSB == 2) {
+        if (n == 2) {
+          f(std::integral_constant<int, 2>{});
+        } else {
+          f(std::integral_constant<int, 1>{});
+        }
+      } else {
+        f(std::integral_constant<int, NSB>{});
+      }
+    };
+    constexpr std::integral_constant<int, NSB> kAllLive{};
 
     // Lazy reference max: probabilities are exp2(s * c - ceil(m_run * c))
     // against a per-row reference m_run that moves only when the row's max
@@ -1479,24 +1495,27 @@ __global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWave
         m_exp = e_new;
       }
     };
-    auto softmax = [&](auto masked_tag, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) {
+    // Softmax of the first L sub-blocks of s into pn (registers 2L and up of
+    // pn are left as they are: P.V and the row sum of this tile skip them).
+    auto softmax = [&](auto masked_tag, auto live_tag, f32x16 (&s)[NSB], u16x8 (&pn)[NSB * 2]) {
       constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr int L = decltype(live_tag)::value;
       float mt = s[0][0];
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
+      for (int sb = 0; sb < L; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
       mt = max_with_other_half(mt);
       rebase(mt);
       const float mc = ceilf(((MASKED && m_run == -INFINITY) ? 0.0f : m_run) * c);
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
+      for (int sb = 0; sb < L; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float pr = fast_exp2(__builtin_fmaf(s[sb][r], c, -mc));
           pn[sb * 2 + (r >> 3)][r & 7] = to_bits(T{}, pr);
         }
-      l_run = add_packed<T>(pn, l_run);
+      l_run = add_packed<T, NSB * 2, 2 * L>(pn, l_run);
     };
 
     // P.V of the pending tile interleaved with the softmax of s: the first
@@ -1671,13 +1690,20 @@ __global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWave
         const int ks = k0 + sb * 32;
         if (ks >= S || (CAUSAL && ks > q0 + 31)) nlive = sb;
       }
-      if (pending) pv(kb ^ 1, pend_live);
+      if (pending) with_live(pend_live, [&](auto lt) __attribute__((always_inline)) { pv(kb ^ 1, lt); });
       if (live) {
-        f32x16 s[NSB];
+        // pn registers past the live sub-blocks are left unset: P.V and the
+        // row sum of this tile never read them.  The copy into pk stays out
+        // of the branches (stores to pk that differ per branch would be
+        // merged into one store at a selected index, which moves pk to
+        // scratch memory).
         u16x8 pn[NSB * 2];
-        qk(std::true_type{}, kb, nlive, s);
-        apply_mask<NSB, CAUSAL>(s, k0, kvalid, qrow, h);
-        softmax(std::true_type{}, s, pn);
+        with_live(nlive, [&](auto lt) __attribute__((always_inline)) {
+          f32x16 s[NSB];
+          qk(lt, kb, s);
+          apply_mask<NSB, CAUSAL, true, decltype(lt)::value>(s, k0, kvalid, qrow, h);
+          softmax(std::true_type{}, lt, s, pn);
+        });
 #pragma unroll
         for (int i = 0; i < NSB * 2; ++i) pk[i] = pn[i];
         pend_live = nlive;
@@ -1702,7 +1728,7 @@ __global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWave
         dma_v_full(kb, t);
         f32x16 s[NSB];
         u16x8 pn[NSB * 2];
-        qk(std::false_type{}, kb, NSB, s);
+        qk(kAllLive, kb, s);
         if constexpr (HAS_MASK) apply_mask<NSB, false>(s, t * BN, kvalid, qrow, h);
         fused(kb ^ 1, s, pn);
 #pragma unroll
@@ -1723,7 +1749,7 @@ __global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWave
         dma_k((t1 + 1) & 1, t1 + 1);
       }
       dma_v_full(t1 & 1, t1);
-      qk(std::false_type{}, t1 & 1, NSB, sa);
+      qk(kAllLive, t1 & 1, sa);
       phase_b(std::false_type{}, kt0 & 1, sa, [](int) {});
       finish_tile(t1);
       // Tile t + 1 for t = t1 .. n_full - 2.
@@ -1780,7 +1806,7 @@ __global__ __launch_bounds__(kThreads, (BNK == 32 ? (D <= 64 ? 4 : 3) : kMinWave
       pend_live = NSB;
     }
     for (int t = max(kt0 + 1, n_full); t < kt1; ++t) generic_tile(t);
-    if (pending) pv((kt1 - 1) & 1, pend_live);
+    if (pending) with_live(pend_live, [&](auto lt) __attribute__((always_inline)) { pv((kt1 - 1) & 1, lt); });
 
     if (BNK == 64 && w.nchunk > 1) {
       // Key-split query tile: publish this chunk's state - per lane the
