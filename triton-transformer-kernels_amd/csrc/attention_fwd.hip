@@ -29,9 +29,13 @@
 //       the softmax VALU of one wavefront runs under the MFMAs of the other
 //       wavefront on the SIMD.
 //     - bf16/fp16: the 8-pass MFMA leaves the softmax as the bound (per
-//       64-key tile a wavefront issues 16 (head_dim 64) or 32 (128) MFMAs
-//       against ~130 VALU instructions, 32 of them v_exp_f32), so the loop
-//       is software-pipelined.  Unmasked tiles run two phases per tile:
+//       64-key tile of the unmasked steady body a wavefront issues 16
+//       (head_dim 64) or 32 (128) MFMAs against 134 other VALU instructions
+//       in the compiled head_dim-64 loop: 114 of softmax (32 fma, 32
+//       v_exp_f32, 16 conversions, 16 max3, 16 dot2 row-sum steps, the
+//       cross-half max), 2 for the lagging-max test and 18 of copy
+//       addressing; a masked tile costs ~280), so the loop is
+//       software-pipelined.  Unmasked tiles run two phases per tile:
 //       Q.K of tile t+1 interleaved with the exp2 and 16-bit rounding of
 //       tile t's scores, then the P.V of tile t interleaved with the row max
 //       of tile t+1.  Key-masked launches run one stream interleaving the
