@@ -505,9 +505,8 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
     for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
 
     // One tile: S^T = K.Q^T, (mask), online softmax, O^T += V^T.P^T.
-    // `nlive` = number of leading 32-key sub-blocks this wavefront needs.
-    // MASKED: apply the key / causal mask; PARTIAL: only the first `nlive`
-    // sub-blocks hold keys this wavefront may see (the others are skipped).
+    // MASKED: apply the key / causal mask; PARTIAL: only the first of the two
+    // sub-blocks holds keys this wavefront may see (the other is skipped).
     // Tiles with every sub-block live keep the branch-free, interleaved
     // sub-block chains even when masked.
     // SB0: index in the LDS tile of the first sub-block processed (k0 and
@@ -517,39 +516,56 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       constexpr bool MASKED = decltype(masked_tag)::value;
       constexpr bool PARTIAL = decltype(partial_tag)::value;
       constexpr int SB0 = decltype(sb0_tag)::value;
+      // Live sub-blocks (nlive, 1 on partial tiles, which have two) as a
+      // compile-time count: a run-time one puts every MFMA of sub-block 1
+      // under its own branch, and the compiler copies its operands through
+      // each (head_dim 64 causal: 337 -> 271 moves, config 2 -0.6 %).
+      // Kernels that never run a partial tile at the measured shapes keep
+      // the run-time form: non-causal (partial only at a ragged end) and
+      // head dim 128 causal (one-sub-block tiles).  Their register
+      // allocation moved with the shape of that dead path, and they ran
+      // 0.8 % (non-causal head_dim 64) and 2-3 % (causal head_dim 128)
+      // slower.
+      constexpr bool kStaticLive = CAUSAL && D < 128;
+      constexpr int NL = (PARTIAL && NSB == 2) ? 1 : NSB;
+      auto live = [&](int sb) __attribute__((always_inline)) {
+        return kStaticLive ? sb < NL : (!PARTIAL || sb < nlive);
+      };
       f32x16 s[NSB];
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) s[sb] = f32x16{};
+      for (int sb = 0; sb < NSB; ++sb)
+        if (!kStaticLive || sb < NL) s[sb] = f32x16{};
       // ---- S^T = K . Q^T (K fragments read one group ahead) --------------
       f32x4 kf[NSB];
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
-        if (!PARTIAL || sb < nlive) kf[sb] = kread(buf, SB0 + sb, 0);
+        if (live(sb)) kf[sb] = kread(buf, SB0 + sb, 0);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         f32x4 kn[NSB];
         if (g + 1 < G) {
 #pragma unroll
           for (int sb = 0; sb < NSB; ++sb)
-            if (!PARTIAL || sb < nlive) kn[sb] = kread(buf, SB0 + sb, g + 1);
+            if (live(sb)) kn[sb] = kread(buf, SB0 + sb, g + 1);
         }
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb) {
-          if (PARTIAL && sb >= nlive) continue;
+          if (!live(sb)) continue;
 #pragma unroll
           for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kf[sb][e], qf[g][e], s[sb]);
         }
         if (g + 1 < G) {
 #pragma unroll
-          for (int sb = 0; sb < NSB; ++sb) kf[sb] = kn[sb];
+          for (int sb = 0; sb < (kStaticLive ? NL : NSB); ++sb) kf[sb] = kn[sb];
         }
         fence();
       }
-      if constexpr (MASKED) apply_mask<NSB, CAUSAL>(s, k0, kvalid, qrow, h);
+      constexpr int NS = kStaticLive ? NL : NSB;  // sub-blocks the softmax visits
+      if constexpr (MASKED) apply_mask<NSB, CAUSAL, true, NS>(s, k0, kvalid, qrow, h);
       // ---- online softmax (exp2 domain) ------------------------------------
       float mt = s[0][0];
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
+      for (int sb = 0; sb < NS; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
       mt = max_with_other_half(mt);
@@ -559,7 +575,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
       const float alpha = fast_exp2(m_run - m_use);
       float ls = 0.0f;
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
+      for (int sb = 0; sb < NS; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float pr = fast_exp2(s[sb][r] - m_use);
@@ -595,7 +611,7 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
         const bool d_ok = (lane & 15) < D;
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb) {
-          if (PARTIAL && sb >= nlive) continue;
+          if (!live(sb)) continue;
           const float* vb = &smV[buf][((SB0 + sb) * 32 + vkey) * D + (lane & 15 & (D - 1))];
 #pragma unroll
           for (int r = 0; r < 16; r += 2) {
@@ -617,17 +633,18 @@ __global__ __launch_bounds__(kThreads, (kMinWaves<true, D>)) void attn_fwd_f32_k
         return;
       }
       // ---- O^T += V^T . P^T (V fragments read one k-step ahead) -----------
-      const int nsteps = (PARTIAL ? nlive : NSB) * 16;
+      const int nsteps = kStaticLive ? NL * 16 : (PARTIAL ? nlive : NSB) * 16;
       VF vf = vread(buf, SB0, 0);
 #pragma unroll
       for (int idx = 0; idx < NSB * 16; ++idx) {
         // Fixed trip count (fully unrolled, so s[][] stays in registers); the
-        // masked path skips the k-steps of dead sub-blocks with a uniform guard.
-        if (!PARTIAL || idx < nsteps) {
+        // dead sub-blocks' k-steps are skipped (at compile time below head
+        // dim 128).
+        if (idx < nsteps) {
           const int sb = idx >> 4;
           const int r = idx & 15;
           VF vn{};
-          if (idx + 1 < NSB * 16 && (!PARTIAL || idx + 1 < nsteps)) {
+          if (idx + 1 < NSB * 16 && idx + 1 < nsteps) {
             vn = vread(buf, SB0 + ((idx + 1) >> 4), (idx + 1) & 15);
           }
           const float pr = s[sb][r];
