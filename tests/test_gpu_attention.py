@@ -24,6 +24,7 @@ import pytest
 import torch
 
 from oracle.attention import (
+    _exp2_scale,
     brute_force_attention_f64,
     chunked_kernel_contract_attention,
     kernel_contract_attention,
@@ -879,11 +880,39 @@ def test_determinism_bitwise(gpu_ready):
     assert torch.equal(a, b)
 
 
+def _causal_rounding_attention_fp32_gpu(q, k, v, chunk=2048):
+    """``kernel_rounding_attention`` for causal launches, restated in fp32
+    torch on the GPU so that every row of a full-size launch can be checked:
+    one head and one block of query rows at a time, keys up to the block's
+    last row.  fp32 products and sums stand in for the model's exact
+    products rounded once (a relative difference of ~1e-6, far inside the
+    contract); the callers pin it against the float64 model on sampled rows.
+    Returns float32 [B, S, H, D] on q's device."""
+    batch, seq_len, heads, head_dim = q.shape
+    sign, c = _exp2_scale(head_dim, None)
+    dev = q.device
+    out = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    keys = torch.arange(seq_len, device=dev)
+    for b in range(batch):
+        for h in range(heads):
+            qh = q[b, :, h, :].float() * sign
+            kt = k[b, :, h, :].float().t().contiguous()
+            vh = v[b, :, h, :].float().contiguous()
+            for start in range(0, seq_len, chunk):
+                end = min(seq_len, start + chunk)
+                s = qh[start:end] @ kt[:, :end]
+                s = s.masked_fill(keys[None, :end] > keys[start:end, None], float("-inf"))
+                ref = torch.ceil(s.max(dim=1).values * c)
+                rounded = torch.exp2(s * c - ref[:, None]).to(q.dtype).float()
+                out[b, start:end, h] = (rounded @ vh[:end]) / rounded.sum(dim=1, keepdim=True)
+    return out
+
+
 def test_config5a_long_sequence_bf16_rows_and_memory(gpu_ready):
     # BASELINE config 5a: causal bf16, B=1, H=32, S=16384, D=128, run at full
-    # size.  Query rows are independent, so the chunked oracle on every head
-    # at four row blocks - start, middle and end of the sequence, where the
-    # rows meet 128 to 16384 keys - checks those rows of the full run.
+    # size.  The float64 rounding model on every head at four row blocks -
+    # start, middle and end of the sequence, where the rows meet 128 to 16384
+    # keys - and its fp32 GPU restatement on every row of every head.
     # Memory: the kernel keeps no workspace, so with a caller-owned output a
     # launch allocates nothing at all.
     from transformer_opt.kernels import hip_attention
@@ -905,10 +934,24 @@ def test_config5a_long_sequence_bf16_rows_and_memory(gpu_ready):
     result = out.cpu()
     assert torch.isfinite(result).all()
     pairs = [(0, h) for h in range(heads)]
+    atol, rtol = CONTRACT[torch.bfloat16]
+    with torch.inference_mode():
+        every_row = _causal_rounding_attention_fp32_gpu(qd, kd, vd)
     for rows in (slice(0, 128), slice(5000, 5128), slice(8128, 8256), slice(16256, 16384)):
         reference = kernel_rounding_attention(q, k, v, None, True, heads=pairs, query_rows=rows)
         actual = torch.stack([result[b, rows, h, :] for b, h in pairs])
         assert contract_failures(actual, reference) == 0, f"rows {rows}"
+        # The fp32 GPU restatement meets the contract against the float64 model
+        # on these rows, and stays close on average (its fp32 score sums flip
+        # the bf16 rounding of a few probabilities, as the kernel's do).
+        restated = torch.stack([every_row[b, rows, h, :] for b, h in pairs]).double().cpu()
+        gap = (restated - reference).abs()
+        assert bool(((gap <= atol) | (gap <= rtol * reference.abs())).all()), f"rows {rows}"
+        assert gap.mean().item() < 5e-5, f"rows {rows}: mean gap {gap.mean().item():.3g}"
+    # Every row of every head against the restatement, under the same contract.
+    err = (out.float() - every_row).abs()
+    ok = torch.isfinite(out.float()) & ((err <= atol) | (err <= rtol * every_row.abs()))
+    assert bool(ok.all()), f"failed={int((~ok).sum())}/{ok.numel()} max_abs={err.max().item():.3g}"
 
 
 # ------------------------------------------------------------------ key split --
