@@ -23,8 +23,9 @@ def _check(x: torch.Tensor) -> None:
 
 def _launch(src: torch.Tensor, dst: torch.Tensor) -> None:
     lib = _native.load()
-    status = lib.ttk_gelu_fwd(src.data_ptr(), dst.data_ptr(), _DTYPE_CODE[src.dtype], src.numel(),
-                              torch.cuda.current_stream(src.device).cuda_stream)
+    with torch.cuda.device(src.device):
+        status = lib.ttk_gelu_fwd(src.data_ptr(), dst.data_ptr(), _DTYPE_CODE[src.dtype], src.numel(),
+                                  torch.cuda.current_stream(src.device).cuda_stream)
     _native.check(status, "gelu")
 
 

@@ -66,10 +66,12 @@ def _run(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], ac
     out_features, in_features = w.shape
     rows = xs.numel() // in_features
     y = torch.empty(*x.shape[:-1], out_features, dtype=x.dtype, device=x.device)
-    status = lib.ttk_linear_fwd(xs.data_ptr(), w.data_ptr(), None if b is None else b.data_ptr(),
-                                y.data_ptr(), _CODES[x.dtype], rows, out_features, in_features,
-                                in_features, in_features, out_features, activation,
-                                torch.cuda.current_stream(x.device).cuda_stream)
+    # The launcher sizes its grid from the current device's CU count.
+    with torch.cuda.device(x.device):
+        status = lib.ttk_linear_fwd(xs.data_ptr(), w.data_ptr(), None if b is None else b.data_ptr(),
+                                    y.data_ptr(), _CODES[x.dtype], rows, out_features, in_features,
+                                    in_features, in_features, out_features, activation,
+                                    torch.cuda.current_stream(x.device).cuda_stream)
     _native.check(status, "linear")
     return y
 
