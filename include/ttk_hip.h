@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define TTK_ABI_VERSION 8
+#define TTK_ABI_VERSION 9
 
 /* Bytes of the arrival-counter block that leads every attention workspace
  * (and the library's static scratch): the same for every launch shape. */
@@ -233,6 +233,81 @@ ttk_status ttk_gelu_fwd(const void* x, void* y, int dtype, int64_t n, void* stre
 ttk_status ttk_linear_fwd(const void* x, const void* w, const void* bias, void* y, int dtype,
                           int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
                           int64_t ldy, int activation, void* stream);
+
+/* Bytes of the counter block that leads every ttk_linear_residual_ln_fwd
+ * workspace: the same for every M (one counter per 64 rows of the largest M
+ * the entry point takes). */
+#define TTK_LINEAR_LN_WS_COUNTER_BYTES 65536
+
+/*
+ * Bytes of the workspace ttk_linear_residual_ln_fwd needs for M rows: the
+ * counter block (TTK_LINEAR_LN_WS_COUNTER_BYTES) followed by 1 KB of row
+ * statistics per 64-row block (0 for M <= 0).
+ */
+int64_t ttk_linear_residual_ln_workspace_size(int64_t M);
+
+/*
+ * W [N, K] (16-bit, row stride ldw elements) into the MFMA fragment order
+ * ttk_linear_residual_ln_fwd reads (N * K elements, contiguous): 16-byte
+ * chunk (fb * K/16 + q) * 64 + l holds W[32 fb + l % 32][16 q + 8 (l / 32) .. + 7].
+ * One 1 KB block per (32 rows, 16 k) fragment, so each fragment is one
+ * coalesced load.  Requirements (TTK_EUNSUPPORTED otherwise): dtype TTK_BF16
+ * or TTK_F16, N a multiple of 32, K of 16, w and w_packed 16-byte aligned,
+ * ldw a multiple of 8 and >= K; w_packed must not overlap w (TTK_EINVAL).
+ * A weight that does not change is packed once.
+ */
+ttk_status ttk_linear_pack_weight(const void* w, void* w_packed, int dtype, int64_t N, int64_t K,
+                                  int64_t ldw, void* stream);
+
+/*
+ * Output projection + residual add + LayerNorm in one kernel, bf16 / fp16,
+ * rows of N = 1024:
+ *
+ *   attn_out = round( A W^T + bias )
+ *   r        = round( x + attn_out )                (the residual output)
+ *   y        = round( (r - mean) * rsqrt(var + eps) * gamma + beta )
+ *
+ * A [M, K] (row stride lda), W [N, K] packed by ttk_linear_pack_weight,
+ * bias [N] or NULL, x, r, y [M, N] (row strides ldx, ldr, ldy), gamma [N],
+ * beta [N] or NULL; mean and the biased variance are those of the rounded r
+ * over its N features, in fp32.  These are the dtype boundaries of the
+ * reference's `self._fused_residual_norm(x, out_proj(context), norm2)` in
+ * 16-bit torch.  r equals the eager 16-bit `x + F.linear(A, W, bias)` bit for
+ * bit whenever the projection does; y is deterministic (independent of
+ * scheduling) and agrees with ttk_residual_layernorm_fwd on the same r to
+ * the last rounding step.
+ *
+ * Two workgroups share each 64-row block (one per half of the features) and
+ * exchange their half-row statistics through the workspace; the first to
+ * finish polls for the other at most max_polls times (a negative value takes
+ * the library default, 4096) and otherwise hands its half to the other,
+ * which then normalises the whole block.  Both routes give the same bits.
+ *
+ * workspace: ttk_linear_residual_ln_workspace_size(M) bytes, 4-byte aligned,
+ * its counter block zero before the call; every completed call leaves it
+ * zero and the block sits at the same bytes for every M, so one zero-filled
+ * buffer serves every later call of any shape on one stream.  Calls that
+ * share a workspace must not run concurrently.
+ *
+ * Requirements (TTK_EUNSUPPORTED otherwise): dtype TTK_BF16 or TTK_F16;
+ * N == 1024; K a positive multiple of 128; a, w_packed, x, gamma, beta, r
+ * and y 16-byte aligned, bias 2-byte aligned; lda, ldx, ldr, ldy multiples
+ * of 8 with lda >= K and ldx, ldr, ldy >= N; M * ld * 2 below 2^31 for x, r
+ * and y.  r and y must not overlap each other, an input or the workspace
+ * (TTK_EINVAL).  M == 0 is a no-op.
+ *
+ * Replaces the attention output projection and the first fused residual +
+ * LayerNorm of an encoder block (reference transformer_opt/submission.py:
+ * 497-505 with fused_residual_layer_norm, transformer_opt/kernels/
+ * residual_layer_norm.py:159-237): the projection's output never goes
+ * through HBM and the LayerNorm launch is gone.
+ */
+ttk_status ttk_linear_residual_ln_fwd(const void* a, const void* w_packed, const void* bias,
+                                      const void* x, const void* gamma, const void* beta, void* r,
+                                      void* y, void* workspace, int64_t workspace_bytes, int dtype,
+                                      int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldx,
+                                      int64_t ldr, int64_t ldy, float eps, int max_polls,
+                                      void* stream);
 
 #ifdef __cplusplus
 }

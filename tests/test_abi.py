@@ -20,7 +20,7 @@ HEADER = REPO / "include" / "ttk_hip.h"
 
 def declared_functions() -> list:
     text = HEADER.read_text()
-    return re.findall(r"^\s*(?:const\s+)?[a-z_]+\*?\s+\*?(ttk_[a-z0-9_]+)\s*\(", text, re.MULTILINE)
+    return re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\*?\s+\*?(ttk_[a-z0-9_]+)\s*\(", text, re.MULTILINE)
 
 
 def test_header_declares_the_exported_symbols():
@@ -200,3 +200,53 @@ def test_linear_argument_errors_are_reported_without_launching():
     assert "overlaps" in _native.last_error()
     assert _linear(lib, x=None) == _native.TTK_EINVAL
     assert _linear(lib, M=0) == _native.TTK_OK  # nothing to launch
+
+
+def _linear_ln(lib, **over):
+    # 64 rows, K = 128: a at 1 MiB, packed W at 2 MiB, x / r / y 128 KiB apart.
+    args = dict(a=1 << 20, wp=2 << 20, b=None, x=3 << 20, g=4 << 20, beta=None, r=5 << 20,
+                y=6 << 20, ws=7 << 20, ws_bytes=65536 + 1024, dtype=_native.TTK_BF16, M=64, N=1024, K=128,
+                lda=128, ldx=1024, ldr=1024, ldy=1024, eps=1e-5, polls=-1, stream=None)
+    args.update(over)
+    return lib.ttk_linear_residual_ln_fwd(
+        args["a"], args["wp"], args["b"], args["x"], args["g"], args["beta"], args["r"], args["y"],
+        args["ws"], args["ws_bytes"], args["dtype"], args["M"], args["N"], args["K"], args["lda"],
+        args["ldx"], args["ldr"], args["ldy"], args["eps"], args["polls"], args["stream"])
+
+
+def test_linear_residual_ln_argument_errors_are_reported_without_launching():
+    lib = _native.load()
+    size = lib.ttk_linear_residual_ln_workspace_size
+    # A fixed counter block (the same bytes for every M) + 1 KB of statistics per 64 rows.
+    block = _native.LINEAR_LN_WS_COUNTER_BYTES
+    assert block == 65536
+    assert size(0) == 0 and size(1) == block + 1024 and size(64 * 64) == block + 64 * 1024
+    assert size(64 * 65) == block + 65 * 1024
+    assert _linear_ln(lib, dtype=_native.TTK_F32) == _native.TTK_EUNSUPPORTED
+    assert "not bf16 or fp16" in _native.last_error()
+    assert _linear_ln(lib, N=512, ldx=512, ldr=512, ldy=512) == _native.TTK_EUNSUPPORTED
+    assert "1024" in _native.last_error()
+    assert _linear_ln(lib, K=192, lda=192) == _native.TTK_EUNSUPPORTED
+    assert "multiple of 128" in _native.last_error()
+    assert _linear_ln(lib, M=-1) == _native.TTK_EINVAL
+    assert _linear_ln(lib, ws=None) == _native.TTK_EINVAL
+    assert _linear_ln(lib, ws_bytes=4) == _native.TTK_EINVAL
+    assert "workspace" in _native.last_error()
+    assert _linear_ln(lib, g=(4 << 20) + 8) == _native.TTK_EUNSUPPORTED
+    assert "16-byte aligned" in _native.last_error()
+    assert _linear_ln(lib, b=(8 << 20) + 1) == _native.TTK_EUNSUPPORTED
+    assert _linear_ln(lib, lda=100) == _native.TTK_EUNSUPPORTED
+    assert _linear_ln(lib, M=1 << 20, ws_bytes=1 << 26) == _native.TTK_EUNSUPPORTED
+    assert "2^31" in _native.last_error()
+    assert _linear_ln(lib, y=(5 << 20) + 1024) == _native.TTK_EINVAL  # y inside r
+    assert "overlap" in _native.last_error()
+    assert _linear_ln(lib, r=3 << 20) == _native.TTK_EINVAL  # r on x
+    assert _linear_ln(lib, y=7 << 20) == _native.TTK_EINVAL  # y on the workspace
+    assert _linear_ln(lib, M=0) == _native.TTK_OK  # nothing to launch
+    pack = lib.ttk_linear_pack_weight
+    # (w, w_packed, dtype, N, K, ldw, stream)
+    assert pack(1 << 20, 2 << 20, _native.TTK_F32, 64, 64, 64, None) == _native.TTK_EUNSUPPORTED
+    assert pack(1 << 20, 2 << 20, _native.TTK_BF16, 40, 64, 64, None) == _native.TTK_EUNSUPPORTED
+    assert pack(1 << 20, 2 << 20, _native.TTK_BF16, 64, 64, 60, None) == _native.TTK_EUNSUPPORTED
+    assert pack(1 << 20, (1 << 20) + 4096, _native.TTK_BF16, 64, 64, 64, None) == _native.TTK_EINVAL
+    assert pack(None, 2 << 20, _native.TTK_BF16, 64, 64, 64, None) == _native.TTK_EINVAL

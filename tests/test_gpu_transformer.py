@@ -334,3 +334,44 @@ def test_config5b_huge_batch_encoder_matches_oracle_on_every_element(gpu_ready):
     assert bool(torch.isfinite(got).all())
     res = compare_outputs(ref, got, rtol=0.01, atol=0.001)
     assert res.passed, f"failed={res.failed_elements} max_abs={res.max_abs_error:.3e} at {res.worst_index}"
+
+
+def test_config4_bf16_with_fused_out_projection_norm(gpu_ready):
+    # The opt-in route that runs each block's attention output projection and
+    # its first residual + LayerNorm as one kernel: config 4 at full size in
+    # bf16 through hipGraph replay, every output against the oracle under the
+    # low-precision bound, and the replayed forward equal to the eager one.
+    cfg = TransformerConfig(4, 2048, 1024, 16, 4096, 6, True)
+    baseline, model = build(cfg, dtype=torch.bfloat16, seed=47)
+    model.fuse_out_projection_norm = True
+    baseline = _bf16_rounded_oracle(baseline)
+    x = torch.randn(4, 2048, 1024, generator=torch.Generator().manual_seed(48)).to(torch.bfloat16)
+    with torch.inference_mode():
+        out = model(x.cuda())
+        calls = model.fused_residual_layer_norm_calls
+        eager = model._forward_eager(x.cuda())
+        got = out.float().cpu()
+        ref = baseline(x.float())
+    assert model.cuda_graph_replays == 1
+    assert calls == 12  # 6 blocks x 2 fused residual + LayerNorms per forward
+    assert torch.equal(out, eager)
+    _assert_low_precision_model(got, ref)
+
+
+def test_fp16_key_padding_with_fused_out_projection_norm(gpu_ready):
+    # fp16 with a key-padding mask on the fused route (d_model 1024, two
+    # layers): padded rows stay exact zeros and valid rows meet the bound.
+    cfg = TransformerConfig(2, 300, 1024, 8, 2048, 2, False)
+    baseline, model = build(cfg, dtype=torch.float16, seed=49)
+    model.fuse_out_projection_norm = True
+    baseline.load_state_dict({k: v.to(torch.float16).float() for k, v in baseline.state_dict().items()})
+    lengths = torch.tensor([300, 123])
+    mask = torch.arange(300)[None, :] < lengths[:, None]
+    x = torch.randn(2, 300, 1024, generator=torch.Generator().manual_seed(50))
+    x = x.masked_fill(~mask[..., None], 0).to(torch.float16)
+    with torch.inference_mode():
+        out = model(x.cuda(), mask.cuda())
+        got = out.float().cpu()
+        ref = baseline(x.float(), mask)
+    assert bool((got[~mask] == 0).all())
+    _assert_low_precision_model(got, ref)

@@ -431,3 +431,152 @@ extern "C" ttk_status ttk_linear_fwd(const void* x, const void* w, const void* b
   if (err != hipSuccess) return fail(TTK_ELAUNCH, "linear: launch failed: %s", hipGetErrorString(err));
   return TTK_OK;
 }
+
+namespace {
+constexpr int64_t kLnRowsPerBlock = 64;
+constexpr int64_t kLnWidth = 1024;
+
+constexpr int kLnDefaultPolls = 4096;
+
+// A counter block of fixed size (one counter per 64-row block of the largest
+// M the entry point takes: x, r and y stay below 2^31 bytes, so M < 2^20),
+// then the statistics area (1 KB per 64-row block).  The counters sit at the
+// same bytes for every M, so launches of any shapes can share a workspace.
+constexpr int64_t kLnCounterBytes = ((int64_t{1} << 20) / kLnRowsPerBlock) * 4;
+int64_t ln_counter_bytes(int64_t) { return kLnCounterBytes; }
+static_assert(kLnCounterBytes == TTK_LINEAR_LN_WS_COUNTER_BYTES, "the header's counter block");
+
+}  // namespace
+
+extern "C" int64_t ttk_linear_residual_ln_workspace_size(int64_t M) {
+  if (M <= 0) return 0;
+  return ln_counter_bytes(M) + (M + kLnRowsPerBlock - 1) / kLnRowsPerBlock * 1024;
+}
+
+extern "C" ttk_status ttk_linear_pack_weight(const void* w, void* w_packed, int dtype, int64_t N,
+                                             int64_t K, int64_t ldw, void* stream) {
+  g_error[0] = '\0';
+  if (dtype != TTK_BF16 && dtype != TTK_F16) {
+    return fail(TTK_EUNSUPPORTED, "pack weight: dtype code %d is not bf16 or fp16", dtype);
+  }
+  if (N <= 0 || K <= 0) {
+    return fail(TTK_EINVAL, "pack weight: N and K must be positive (N=%lld K=%lld)", (long long)N,
+                (long long)K);
+  }
+  if (!w || !w_packed) return fail(TTK_EINVAL, "pack weight: w and w_packed must not be NULL");
+  if (N % 32 != 0 || K % 16 != 0) {
+    return fail(TTK_EUNSUPPORTED, "pack weight: N=%lld must be a multiple of 32 and K=%lld of 16",
+                (long long)N, (long long)K);
+  }
+  if (!aligned16(w) || !aligned16(w_packed) || ldw % 8 != 0 || ldw < K) {
+    return fail(TTK_EUNSUPPORTED,
+                "pack weight: w and w_packed must be 16-byte aligned, ldw a multiple of 8 and >= K "
+                "(ldw=%lld)",
+                (long long)ldw);
+  }
+  if (N > (int64_t{1} << 30) || K > (int64_t{1} << 30)) {
+    return fail(TTK_EUNSUPPORTED, "pack weight: N or K too large");
+  }
+  const uint64_t wbytes = (static_cast<uint64_t>(N - 1) * ldw + K) * 2;
+  if (overlaps(w_packed, static_cast<uint64_t>(N) * K * 2, w, wbytes)) {
+    return fail(TTK_EINVAL, "pack weight: w_packed overlaps w");
+  }
+  const hipError_t err = ttk::launch_pack_weight(w, w_packed, static_cast<int>(N), static_cast<int>(K), ldw,
+                                                 static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(TTK_ELAUNCH, "pack weight: launch failed: %s", hipGetErrorString(err));
+  return TTK_OK;
+}
+
+extern "C" ttk_status ttk_linear_residual_ln_fwd(const void* a, const void* w_packed, const void* bias,
+                                                 const void* x, const void* gamma, const void* beta,
+                                                 void* r, void* y, void* workspace,
+                                                 int64_t workspace_bytes, int dtype, int64_t M,
+                                                 int64_t N, int64_t K, int64_t lda, int64_t ldx,
+                                                 int64_t ldr, int64_t ldy, float eps, int max_polls,
+                                                 void* stream) {
+  g_error[0] = '\0';
+  if (dtype != TTK_BF16 && dtype != TTK_F16) {
+    return fail(TTK_EUNSUPPORTED, "linear+LN: dtype code %d is not bf16 or fp16", dtype);
+  }
+  if (M < 0 || N <= 0 || K <= 0) {
+    return fail(TTK_EINVAL, "linear+LN: M must be >= 0 and N, K positive (M=%lld N=%lld K=%lld)",
+                (long long)M, (long long)N, (long long)K);
+  }
+  if (N != kLnWidth) {
+    return fail(TTK_EUNSUPPORTED, "linear+LN: N=%lld; the kernel normalises rows of 1024", (long long)N);
+  }
+  if (K % 128 != 0 || K > (int64_t{1} << 24)) {
+    return fail(TTK_EUNSUPPORTED, "linear+LN: K=%lld must be a positive multiple of 128", (long long)K);
+  }
+  if (M == 0) return TTK_OK;
+  if (!a || !w_packed || !x || !gamma || !r || !y || !workspace) {
+    return fail(TTK_EINVAL, "linear+LN: a, w_packed, x, gamma, r, y and workspace must not be NULL");
+  }
+  if (!aligned16(a) || !aligned16(w_packed) || !aligned16(x) || !aligned16(gamma) || !aligned16(r) ||
+      !aligned16(y) || (beta != nullptr && !aligned16(beta))) {
+    return fail(TTK_EUNSUPPORTED, "linear+LN: a, w_packed, x, gamma, beta, r and y must be 16-byte aligned");
+  }
+  if (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 1u) != 0) {
+    return fail(TTK_EUNSUPPORTED, "linear+LN: bias must be 2-byte aligned");
+  }
+  if ((reinterpret_cast<uintptr_t>(workspace) & 3u) != 0 ||
+      workspace_bytes < ttk_linear_residual_ln_workspace_size(M)) {
+    return fail(TTK_EINVAL, "linear+LN: workspace must be 4-byte aligned and hold %lld bytes (got %lld)",
+                (long long)ttk_linear_residual_ln_workspace_size(M), (long long)workspace_bytes);
+  }
+  if (lda % 8 != 0 || ldx % 8 != 0 || ldr % 8 != 0 || ldy % 8 != 0 || lda < K || ldx < N ||
+      ldr < N || ldy < N) {
+    return fail(TTK_EUNSUPPORTED,
+                "linear+LN: row strides must be multiples of 8 elements with lda >= K and ldx, ldr, "
+                "ldy >= N (lda=%lld ldx=%lld ldr=%lld ldy=%lld)",
+                (long long)lda, (long long)ldx, (long long)ldr, (long long)ldy);
+  }
+  const uint64_t abytes = (static_cast<uint64_t>(M - 1) * lda + K) * 2;
+  const uint64_t xbytes = static_cast<uint64_t>(M) * ldx * 2;
+  const uint64_t rbytes = static_cast<uint64_t>(M) * ldr * 2;
+  const uint64_t ybytes = static_cast<uint64_t>(M) * ldy * 2;
+  if (xbytes >= (uint64_t{1} << 31) || rbytes >= (uint64_t{1} << 31) || ybytes >= (uint64_t{1} << 31) ||
+      M > (int64_t{1} << 30)) {
+    return fail(TTK_EUNSUPPORTED, "linear+LN: x, r or y spans 2^31 bytes or more (M=%lld)", (long long)M);
+  }
+  const uint64_t wbytes = static_cast<uint64_t>(N) * K * 2;
+  const uint64_t ws_used = static_cast<uint64_t>(ttk_linear_residual_ln_workspace_size(M));
+  struct Span {
+    const void* p;
+    uint64_t n;
+  };
+  const Span inputs[] = {{a, abytes}, {w_packed, wbytes}, {x, xbytes}, {gamma, static_cast<uint64_t>(N) * 2},
+                         {beta, beta ? static_cast<uint64_t>(N) * 2 : 0},
+                         {bias, bias ? static_cast<uint64_t>(N) * 2 : 0}, {workspace, ws_used}};
+  for (const Span& in : inputs) {
+    if (in.p != nullptr && (overlaps(r, rbytes, in.p, in.n) || overlaps(y, ybytes, in.p, in.n))) {
+      return fail(TTK_EINVAL, "linear+LN: r or y overlaps an input or the workspace");
+    }
+  }
+  if (overlaps(r, rbytes, y, ybytes)) return fail(TTK_EINVAL, "linear+LN: r overlaps y");
+  ttk::LinearLnParams p{};
+  p.a = a;
+  p.wp = w_packed;
+  p.bias = bias;
+  p.x = x;
+  p.gamma = gamma;
+  p.beta = beta;
+  p.r = r;
+  p.y = y;
+  p.counters = static_cast<int*>(workspace);
+  p.stats = reinterpret_cast<float*>(static_cast<char*>(workspace) + ln_counter_bytes(M));
+  p.max_polls = max_polls < 0 ? kLnDefaultPolls : max_polls;
+  p.lda = lda;
+  p.ldx = ldx;
+  p.ldr = ldr;
+  p.ldy = ldy;
+  p.M = static_cast<int>(M);
+  p.K = static_cast<int>(K);
+  p.eps = eps;
+  p.x_bytes = static_cast<unsigned>(xbytes);
+  p.r_bytes = static_cast<unsigned>(rbytes);
+  p.y_bytes = static_cast<unsigned>(ybytes);
+  const hipError_t err = ttk::launch_linear_ln(dtype, p, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(TTK_ELAUNCH, "linear+LN: launch failed: %s", hipGetErrorString(err));
+  return TTK_OK;
+}

@@ -149,6 +149,28 @@ struct LinearParams {
   unsigned y_bytes;  // bytes of Y addressed by the store resource
 };
 
+// Launch parameters of the Linear + residual + LayerNorm kernel (width 1024):
+// attn_out = round(A W^T + bias), r = round(x + attn_out),
+// y = round(LayerNorm(r) * gamma + beta); A [M, K], W packed in fragment
+// order, x / r / y [M, 1024], element leading dimensions.
+struct LinearLnParams {
+  const void* a;
+  const void* wp;     // W [1024, K] packed by launch_pack_weight
+  const void* bias;   // [1024] or null
+  const void* x;
+  const void* gamma;  // [1024]
+  const void* beta;   // [1024] or null
+  void* r;
+  void* y;
+  int* counters;      // one per 64-row block: zero before a launch, left zero
+  float* stats;       // 256 floats per 64-row block: the halves' row statistics
+  int64_t lda, ldx, ldr, ldy;
+  int M, K;
+  float eps;
+  int max_polls;      // polls of the first workgroup of a pair for the second
+  unsigned x_bytes, r_bytes, y_bytes;  // extents of the buffer resources
+};
+
 // Host-side launchers (defined next to their kernels).  Return a HIP error.
 // launch_attention fills p.pair / p.units / the split plan and sizes the
 // grid itself.  `workspace` (workspace_bytes, 256-byte aligned) may be null;
@@ -170,5 +192,12 @@ hipError_t launch_gelu(int dtype, const void* x, void* y, int64_t n, hipStream_t
 // Linear + activation (0 none, 1 exact GELU) for dtype 1 (bf16) or 2 (fp16);
 // fills the tile fields of p and sizes the grid.
 hipError_t launch_linear(int dtype, int activation, LinearParams& p, hipStream_t stream);
+
+// Linear + residual + LayerNorm, dtype 1 (bf16) or 2 (fp16).
+hipError_t launch_linear_ln(int dtype, LinearLnParams& p, hipStream_t stream);
+// W [N, K] (16-bit, row stride ldw) into MFMA fragment order (N % 32 == 0,
+// K % 16 == 0): 16-byte chunk (fb * K/16 + q) * 64 + l holds
+// W[32 fb + l % 32][16 q + 8 (l / 32) .. + 7].
+hipError_t launch_pack_weight(const void* w, void* wp, int N, int K, int64_t ldw, hipStream_t stream);
 
 }  // namespace ttk

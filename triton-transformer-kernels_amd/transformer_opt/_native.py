@@ -39,11 +39,17 @@ EXPORTED_SYMBOLS = (
     "ttk_residual_layernorm_fwd",
     "ttk_gelu_fwd",
     "ttk_linear_fwd",
+    "ttk_linear_residual_ln_workspace_size",
+    "ttk_linear_pack_weight",
+    "ttk_linear_residual_ln_fwd",
 )
-ABI_VERSION = 8
+ABI_VERSION = 9
 # TTK_ATTENTION_WS_COUNTER_BYTES: the zero-initialised counter block that
 # leads every attention workspace, the same for every launch shape.
 ATTENTION_WS_COUNTER_BYTES = 16384
+# TTK_LINEAR_LN_WS_COUNTER_BYTES: the counter block that leads every
+# linear + residual + LayerNorm workspace, the same for every M.
+LINEAR_LN_WS_COUNTER_BYTES = 65536
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -92,6 +98,15 @@ def _configure(lib: ctypes.CDLL) -> None:
     lib.ttk_linear_fwd.restype = ctypes.c_int
     lib.ttk_linear_fwd.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i64, _i64, _i64, _i64,
                                    _i64, ctypes.c_int, _vp]
+    lib.ttk_linear_residual_ln_workspace_size.restype = _i64
+    lib.ttk_linear_residual_ln_workspace_size.argtypes = [_i64]
+    lib.ttk_linear_pack_weight.restype = ctypes.c_int
+    lib.ttk_linear_pack_weight.argtypes = [_vp, _vp, ctypes.c_int, _i64, _i64, _i64, _vp]
+    lib.ttk_linear_residual_ln_fwd.restype = ctypes.c_int
+    lib.ttk_linear_residual_ln_fwd.argtypes = [
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, ctypes.c_int,
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _vp,
+    ]
 
 
 def load() -> ctypes.CDLL:

@@ -89,6 +89,30 @@ class PackedQKV:
         return self.stamp == PackedQKV.stamp_of(tuple(weights) + tuple(biases))
 
 
+class PackedOut:
+    """The attention output projection's weight in the MFMA fragment order of
+    the fused projection + residual + LayerNorm kernel, rebuilt whenever the
+    weight changes (same rule as ``PackedQKV``).  ``packed`` is None when that
+    kernel cannot take the weight (not a 16-bit [1024, K] ROCm tensor with K a
+    multiple of 128)."""
+
+    __slots__ = ("sources", "stamp", "packed")
+
+    def __init__(self, weight: torch.Tensor):
+        from .kernels.linear_ln import WIDTH, pack_weight
+
+        self.sources = (weight,)
+        self.stamp = PackedQKV.stamp_of(self.sources)
+        self.packed = None
+        if (weight.is_cuda and weight.dtype in (torch.bfloat16, torch.float16) and weight.ndim == 2
+                and weight.shape[0] == WIDTH and weight.shape[1] % 128 == 0):
+            with torch.no_grad():
+                self.packed = pack_weight(weight.detach())
+
+    def serves(self, weight: torch.Tensor) -> bool:
+        return self.stamp is not None and self.stamp == PackedQKV.stamp_of((weight,))
+
+
 _CAPTURE_STREAMS: Dict[int, torch.cuda.Stream] = {}
 _CAPTURE_STREAMS_LOCK = threading.Lock()
 
@@ -183,6 +207,7 @@ class ReplayCache:
         self.entries: "OrderedDict[Hashable, CapturedForward]" = OrderedDict()
         self.last: Optional[CapturedForward] = None
         self.packs: Dict[int, PackedQKV] = {}
+        self.out_packs: Dict[int, PackedOut] = {}
         # The model's module-tree layout and the operands resolved from it,
         # with the (layout epoch, tensor stamps, scalars) key they were
         # resolved under; owned by the model, cached here so copies start
@@ -208,6 +233,7 @@ class ReplayCache:
         with self.lock:
             self.drop_captures()
             self.packs.clear()
+            self.out_packs.clear()
             self.layout = None
             self.operands = None
             self.operands_key = None
@@ -217,6 +243,13 @@ class ReplayCache:
         if pack is None or not pack.serves(weights, biases):
             pack = PackedQKV(weights, biases)
             self.packs[slot] = pack
+        return pack
+
+    def out_pack_for(self, slot: int, weight: torch.Tensor) -> PackedOut:
+        pack = self.out_packs.get(slot)
+        if pack is None or not pack.serves(weight):
+            pack = PackedOut(weight)
+            self.out_packs[slot] = pack
         return pack
 
     def entry(self, fingerprint: Hashable, geometry: Hashable,

@@ -57,6 +57,8 @@ from .config import ATTENTION_BACKENDS, SUPPORTED_DTYPES
 from .dispatch import attention_forward
 from .kernels.gelu import gelu_
 from .kernels.linear import linear_gelu, linear_supported
+from .kernels.linear_ln import linear_ln_supported, linear_residual_layer_norm
+from .kernels.linear_ln import workspace_bytes as linear_ln_workspace_bytes
 from .kernels.residual_layer_norm import fused_residual_layer_norm, layer_norm
 from .model import TransformerBlock, TransformerConfig
 from .replay import CapturedForward, ReplayCache
@@ -88,6 +90,9 @@ class _Block(NamedTuple):
     ffn_out_weight: torch.Tensor
     ffn_out_bias: Optional[torch.Tensor]
     exit_norm: _Norm  # the next block's norm1, or the final norm
+    # out_weight packed for the fused projection + residual + LayerNorm
+    # kernel, or None when that kernel cannot take it.
+    out_packed: Optional[torch.Tensor]
 
 
 class _Operands(NamedTuple):
@@ -176,12 +181,14 @@ class _Layout:
         for index, (entry, attn) in enumerate(zip(self.layers, self.attentions)):
             qkv = entry["qkv"]
             pack = cache.pack_for(index, qkv[:3], qkv[3:])
+            out_pack = cache.out_pack_for(index, entry["out"][0])
             blocks.append(_Block(
                 pack.weight, pack.bias, attn.num_heads, attn.head_dim, attn.scale,
                 *entry["out"], _Norm(*entry["norm2"], eps[2 * index + 1]),
-                *entry["ffn_in"], *entry["ffn_out"], exits[index + 1],
+                *entry["ffn_in"], *entry["ffn_out"], exits[index + 1], out_pack.packed,
             ))
-        keepalive = (self.tensors, tuple(cache.packs.values()))
+        keepalive = (self.tensors, tuple(cache.packs.values()),
+                     tuple(p.packed for p in cache.out_packs.values()))
         return _Operands(exits[0], tuple(blocks), None, keepalive)
 
 
@@ -226,6 +233,11 @@ class UserOptimizedTransformer(nn.Module):
         self.cuda_graph_replays = 0
         self.attention_backend_counts: Dict[str, int] = {"hip": 0, "reference": 0}
         self.fused_residual_layer_norm_calls = 0
+        # True: in bf16/fp16 models of width 1024, each block's attention
+        # output projection and its first residual + LayerNorm run as one HIP
+        # kernel.  Off by default: at config 4 the library GEMM plus the
+        # residual + LayerNorm kernel is faster.
+        self.fuse_out_projection_norm = False
         # Captures, packed projections and the lock: derived inference state,
         # outside the state dict and not copied with the module.
         self._replay = ReplayCache(max_cuda_graphs)
@@ -294,7 +306,8 @@ class UserOptimizedTransformer(nn.Module):
             cache.operands, cache.operands_key = ops, key
         fingerprint = None
         if stamps is not None and settled:
-            fingerprint = key + (self.config, torch.backends.cuda.matmul.allow_tf32)
+            fingerprint = key + (self.config, torch.backends.cuda.matmul.allow_tf32,
+                                 self.fuse_out_projection_norm)
         return ops._replace(fingerprint=fingerprint)
 
     # -- the forward ----------------------------------------------------------------
@@ -313,21 +326,42 @@ class UserOptimizedTransformer(nn.Module):
         masked = mask is not None
         h = layer_norm(x, *ops.entry_norm)
         last = len(ops.blocks) - 1
+        workspace = None
         for index, block in enumerate(ops.blocks):
-            x, h = self._fused_norm(x, self._attend(block, h, mask, tally), block.norm2, mask,
-                                    tally)
+            context = self._attend(block, h, mask, tally)
+            norm = block.norm2
+            if (self.fuse_out_projection_norm and block.out_packed is not None
+                    and linear_ln_supported(context, block.out_packed, block.out_bias, x,
+                                            norm.weight, norm.bias) is None):
+                # One zeroed workspace serves the forward's launches in turn
+                # (each leaves its counters zero); under capture it comes
+                # from the graph's pool and is cleared inside the graph.
+                if workspace is None:
+                    workspace = torch.zeros(linear_ln_workspace_bytes(x.numel() // x.shape[-1]),
+                                            dtype=torch.uint8, device=x.device)
+                # The block's first residual + LayerNorm zeroes nothing, so
+                # the key mask does not enter it.
+                x, h = linear_residual_layer_norm(context, block.out_packed, block.out_bias, x,
+                                                  norm.weight, norm.bias, norm.eps,
+                                                  workspace=workspace)
+                tally.count_fused_norm()
+            else:
+                update = F.linear(context, block.out_weight, block.out_bias)
+                x, h = self._fused_norm(x, update, norm, mask, tally)
             x, h = self._fused_norm(x, self._feed_forward(block, h), block.exit_norm, mask, tally,
                                     zero_residual=masked, zero_output=masked and index == last)
         return h
 
     def _attend(self, block: _Block, h: torch.Tensor, mask, tally) -> torch.Tensor:
+        """Multi-head attention of one block up to its output projection:
+        the context ``[B, S, width]`` that out_proj maps."""
         batch, seq_len, width = h.shape
         qkv = F.linear(h, block.qkv_weight, block.qkv_bias)
         q, k, v = qkv.view(batch, seq_len, 3, block.num_heads, block.head_dim).unbind(2)
         context, record = attention_forward(q, k, v, mask, causal=self.config.causal,
                                             scale=block.scale, backend=self.attention_backend)
         tally.count_attention(record.selected)
-        return F.linear(context.view(batch, seq_len, width), block.out_weight, block.out_bias)
+        return context.view(batch, seq_len, width)
 
     @staticmethod
     def _feed_forward(block: _Block, h: torch.Tensor) -> torch.Tensor:
