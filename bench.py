@@ -156,6 +156,24 @@ def ffn_input_operands():
     return x, w, b
 
 
+def out_projection_norm_operands():
+    """The config-4 encoder's attention output projection and the residual +
+    LayerNorm after it, bf16: context and residual [8192, 1024] ~ N(0, 1),
+    Xavier-uniform weight [1024, 1024], biases ~ N(0, 0.02), gamma ~ U(0.5,
+    1.5), beta ~ N(0, 0.1)."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    a = torch.randn(8192, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    bound = (6.0 / 2048) ** 0.5
+    w = ((torch.rand(1024, 1024, device="cuda", generator=g) * 2 - 1) * bound).to(torch.bfloat16)
+    b = (torch.randn(1024, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(8192, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    gamma = (torch.rand(1024, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+    beta = (torch.randn(1024, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+    return a, w, b, x, gamma, beta
+
+
 def ffn_input_ab(steps: int = 50, warmup: int = 10) -> dict:
     """Per-call times (us) of the config-4 FFN input in bf16: the fused Linear +
     exact-GELU kernel against what it replaces (library GEMM, then the
@@ -465,6 +483,18 @@ def profile_only(which: str, steps: int, warmup: int, seq_len: int = 1024, hidde
         else:
             fn = lambda: gelu_(torch.nn.functional.linear(x, w, b))  # noqa: E731
         work = 2.0 * 8192 * 4096 * 1024
+    elif which in ("linear_ln", "linear_ln_pair"):
+        from transformer_opt.kernels import fused_residual_layer_norm
+        from transformer_opt.kernels.linear_ln import linear_residual_layer_norm, pack_weight
+
+        a, w, b, x, gamma, beta = out_projection_norm_operands()
+        if which == "linear_ln":
+            wp = pack_weight(w)
+            fn = lambda: linear_residual_layer_norm(a, wp, b, x, gamma, beta, 1e-5)  # noqa: E731
+        else:
+            fn = lambda: fused_residual_layer_norm(  # noqa: E731
+                x, torch.nn.functional.linear(a, w, b), gamma, beta, 1e-5)
+        work = 2.0 * 8192 * 1024 * 1024
     elif which in ("encoder_fp32", "encoder_bf16"):
         from transformer_opt.submission import TransformerConfig, UserOptimizedTransformer
 
@@ -539,7 +569,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--profile-only", choices=("attention", "layernorm", "layernorm_bf16", "copy", "attention_bf16",
                                                    "attention_bf16_d64", "attention_5b", "encoder_fp32", "encoder_bf16",
-                                                   "encoder_5b", "gelu", "linear_gelu", "linear_gelu_pair"),
+                                                   "encoder_5b", "gelu", "linear_gelu", "linear_gelu_pair",
+                                                   "linear_ln", "linear_ln_pair"),
                         help="launch only one kernel (warmup + steps) for rocprofv3 runs; prints its timing")
     parser.add_argument("--seq-len", type=int, default=1024,
                         help="sequence length of --profile-only attention (B=8, H=16, D=64, fp32)")
