@@ -173,7 +173,10 @@ class _Layout:
         return (tuple([n.eps for n in self.norms]),
                 tuple([(a.num_heads, a.head_dim, a.d_model, a.scale) for a in self.attentions]))
 
-    def resolve(self, cache: ReplayCache) -> _Operands:
+    def resolve(self, cache: ReplayCache, fuse_out: bool) -> _Operands:
+        """Operands of every block; the out-projection weights are packed for
+        the fused projection + residual + LayerNorm kernel only with
+        ``fuse_out`` (otherwise the packs are dropped)."""
         eps = [n.eps for n in self.norms]
         exits = [_Norm(*entry["norm1"], eps[2 * i]) for i, entry in enumerate(self.layers)]
         exits.append(_Norm(*self.final_norm, eps[-1]))
@@ -181,12 +184,14 @@ class _Layout:
         for index, (entry, attn) in enumerate(zip(self.layers, self.attentions)):
             qkv = entry["qkv"]
             pack = cache.pack_for(index, qkv[:3], qkv[3:])
-            out_pack = cache.out_pack_for(index, entry["out"][0])
+            out_packed = cache.out_pack_for(index, entry["out"][0]).packed if fuse_out else None
             blocks.append(_Block(
                 pack.weight, pack.bias, attn.num_heads, attn.head_dim, attn.scale,
                 *entry["out"], _Norm(*entry["norm2"], eps[2 * index + 1]),
-                *entry["ffn_in"], *entry["ffn_out"], exits[index + 1], out_pack.packed,
+                *entry["ffn_in"], *entry["ffn_out"], exits[index + 1], out_packed,
             ))
+        if not fuse_out:
+            cache.out_packs.clear()
         keepalive = (self.tensors, tuple(cache.packs.values()),
                      tuple(p.packed for p in cache.out_packs.values()))
         return _Operands(exits[0], tuple(blocks), None, keepalive)
@@ -299,15 +304,15 @@ class UserOptimizedTransformer(nn.Module):
         scalars = layout.scalars()
         settled = not any(m.training or m._forward_hooks or m._forward_pre_hooks
                           for m in (self,) + layout.modules)
-        key = (layout.epoch, stamps, scalars)
+        fuse_out = bool(self.fuse_out_projection_norm)
+        key = (layout.epoch, stamps, scalars, fuse_out)
         ops = cache.operands
         if ops is None or stamps is None or cache.operands_key != key:
-            ops = layout.resolve(cache)
+            ops = layout.resolve(cache, fuse_out)
             cache.operands, cache.operands_key = ops, key
         fingerprint = None
         if stamps is not None and settled:
-            fingerprint = key + (self.config, torch.backends.cuda.matmul.allow_tf32,
-                                 self.fuse_out_projection_norm)
+            fingerprint = key + (self.config, torch.backends.cuda.matmul.allow_tf32)
         return ops._replace(fingerprint=fingerprint)
 
     # -- the forward ----------------------------------------------------------------
