@@ -1,9 +1,9 @@
 """Invariants of the generated gfx950 code that the kernels rely on (CPU only).
 
-The attention kernels issue their global->LDS copies as inline assembly
-that writes M0 (the LDS address of the copy).  M0 is a register the compiler
-reserves, so the copies are only safe while no compiler-generated instruction
-of those kernels uses M0: the first test compiles the source to gfx950
+The attention and linear kernels issue their global->LDS copies as inline
+assembly that writes M0 (the LDS address of the copy).  M0 is a register the
+compiler reserves, so the copies are only safe while no compiler-generated
+instruction of those kernels uses M0: the first test compiles each source to gfx950
 assembly (hipcc, no GPU needed) and checks that every reference to m0 sits
 inside an inline-assembly block.  The second checks the buffer offsets the
 short-sequence kernels rely on for their row bounds.
@@ -33,7 +33,7 @@ def _assembly(source: Path, tmp_path: Path) -> str:
     return out.read_text()
 
 
-@pytest.mark.parametrize("name", ["attention_fwd.hip"])
+@pytest.mark.parametrize("name", ["attention_fwd.hip", "linear_fwd.hip"])
 def test_m0_is_only_written_by_the_inline_copies(tmp_path, name):
     text = _assembly(CSRC / name, tmp_path)
     inside = outside = 0
