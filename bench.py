@@ -199,6 +199,33 @@ def ffn_input_ab(steps: int = 50, warmup: int = 10) -> dict:
     return out
 
 
+def out_projection_norm_ab(steps: int = 50, warmup: int = 10) -> dict:
+    """Per-call times (us) of the config-4 attention output projection and the
+    residual + LayerNorm after it, bf16: the fused kernel (an opt-in model
+    route) against the library GEMM followed by the residual + LayerNorm
+    kernel (the model's default), alternating twice, best of each."""
+    import torch
+    import torch.nn.functional as F
+
+    from transformer_opt.kernels import fused_residual_layer_norm
+    from transformer_opt.kernels.linear_ln import linear_residual_layer_norm, pack_weight
+
+    a, w, b, x, gamma, beta = out_projection_norm_operands()
+    best = {}
+    with torch.inference_mode():
+        wp = pack_weight(w)
+        routes = {"fused_linear_residual_ln": lambda: linear_residual_layer_norm(a, wp, b, x, gamma, beta, 1e-5),
+                  "library_gemm_then_residual_ln": lambda: fused_residual_layer_norm(
+                      x, F.linear(a, w, b), gamma, beta, 1e-5)}
+        for _ in range(2):
+            for name, fn in routes.items():
+                us = back_to_back_ms(fn, steps, warmup) * 1e3
+                best[name] = min(best.get(name, us), us)
+    out = {name: {"us": round(us, 2)} for name, us in best.items()}
+    out["fused_speedup_vs_pair"] = round(best["library_gemm_then_residual_ln"] / best["fused_linear_residual_ln"], 3)
+    return out
+
+
 def attention_tflops(batch, seq_len, heads, head_dim, causal, dtype, steps=10, warmup=3):
     from transformer_opt.kernels import hip_attention
 
@@ -747,6 +774,10 @@ def main() -> int:
         ffn = ffn_input_ab()
         secondary["ffn_input_bf16_8192x4096x1024"] = ffn
         log(f"FFN input bf16: {ffn}")
+        torch.cuda.empty_cache()
+        proj = out_projection_norm_ab()
+        secondary["out_projection_residual_ln_bf16_8192x1024x1024"] = proj
+        log(f"out projection + residual + LN bf16: {proj}")
         torch.cuda.empty_cache()
         model = {}
         for dtype_name in ("fp32", "bf16"):
