@@ -31,12 +31,12 @@
 //   holds 8 consecutive features of one token), the residual add with x and
 //   its rounding, r stored.  Each workgroup then forms the statistics of its
 //   half of every row (sum S and centred sum of squares M2) and publishes
-//   them (system-scope atomic stores, then a release fence: the two halves
-//   run on different XCDs, whose L2 caches are not coherent, and only the
-//   fence's L2 write-back makes the stores visible to the other XCD before
-//   the count), counts itself in on its row block's
-//   counter and, once both are in, merges the two halves' statistics and
-//   writes y for its own half.  The first of a pair polls for the second a
+//   them (system-scope atomic stores; the two halves run on different XCDs,
+//   whose L2 caches are not coherent), then an agent-scope release fence
+//   (L2 write-back and the wait for it, the memory model's release) orders
+//   them before the workgroup counts itself in on its row block's counter.
+//   Once both are in, each merges the two halves' statistics and writes y
+//   for its own half.  The first of a pair polls for the second a
 //   bounded number of times; if the second does not come, the first makes
 //   its r visible (a release fence) and hands its half over (a
 //   compare-and-swap on the counter), and the second then normalises both
@@ -301,9 +301,8 @@ __global__ __launch_bounds__(64 * kLlnWaves) void linear_ln_kernel(LinearLnParam
         __hip_atomic_store(st + 1, own_m2[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
     }
-    // Waiting for the stores to complete is not enough for another XCD to
-    // see them once it sees the count: a release fence (L2 write-back, then
-    // the wait for it) orders them before the count-in below.
+    // The release that orders the statistics before the count-in below
+    // (agent scope: L2 write-back, then the wait for it).
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   }
 
