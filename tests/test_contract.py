@@ -285,3 +285,28 @@ def test_harness_accuracy_loop_uses_the_or_rule(capsys):
     assert not run_accuracy_tests(model, Shifted(model, 0.5), **args)
     out = capsys.readouterr().out
     assert "trial 01/2: PASS" in out and "summary: FAIL" in out and "worst_index=" in out
+
+
+def test_fused_out_projection_norm_route_contract():
+    # The opt-in projection + residual + LayerNorm route: off by default,
+    # never packs a weight the kernel cannot take (a CPU weight here), packs
+    # nothing while the route is off, and its support check explains refusals
+    # before any device work.
+    from transformer_opt.kernels.linear_ln import linear_ln_supported, pack_weight
+    from transformer_opt.replay import PackedOut
+
+    cfg = TransformerConfig(1, 16, 1024, 8, 64, 1, False)
+    model = UserOptimizedTransformer(cfg).to(torch.bfloat16).eval()
+    assert model.fuse_out_projection_norm is False
+    ops = model._operands()
+    assert all(block.out_packed is None for block in ops.blocks) and not model._replay.out_packs
+    model.fuse_out_projection_norm = True
+    ops = model._operands()
+    assert all(block.out_packed is None for block in ops.blocks)  # CPU weights: nothing to pack
+    assert PackedOut(torch.zeros(1024, 1024, dtype=torch.bfloat16)).packed is None
+    a = torch.zeros(16, 1024, dtype=torch.bfloat16)
+    x = torch.zeros(16, 1024, dtype=torch.bfloat16)
+    g = torch.ones(1024, dtype=torch.bfloat16)
+    assert "ROCm" in linear_ln_supported(a, torch.zeros(1024 * 1024, dtype=torch.bfloat16), None, x, g, None)
+    with pytest.raises(ValueError, match="ROCm"):
+        pack_weight(torch.zeros(1024, 1024, dtype=torch.bfloat16))
