@@ -166,3 +166,30 @@ def test_linear_rejects_what_it_cannot_run(gpu_ready):
             linear_gelu(x, w)
     with pytest.raises(ValueError, match="multiple of 128"):
         linear_gelu(x[:, :128].contiguous(), torch.randn(64, 128, device="cuda", dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("case_seed", range(12))
+def test_random_shapes_against_float64(gpu_ready, case_seed):
+    # Seeded sweep over the envelope: M from 1 to 1500 (ragged token tiles),
+    # N a multiple of 32 up to 1184 (partial feature tiles), K a multiple of
+    # 128 from 256 to 1536, with and without bias, both activations and both
+    # dtypes, inputs scaled by a random factor.
+    from transformer_opt.kernels.linear import linear, linear_gelu
+
+    rng = np.random.default_rng(1000 + case_seed)
+    rows = int(rng.integers(1, 1501))
+    out_features = 32 * int(rng.integers(1, 38))
+    in_features = 128 * int(rng.integers(2, 13))
+    dtype = (torch.bfloat16, torch.float16)[case_seed % 2]
+    gelu = bool(rng.integers(0, 2))
+    bias = bool(rng.integers(0, 2))
+    scale = float(rng.choice([0.25, 1.0, 3.0]))
+    g = torch.Generator().manual_seed(case_seed)
+    x = (torch.randn(rows, in_features, generator=g) * scale).to(dtype)
+    w = (torch.randn(out_features, in_features, generator=g) * in_features ** -0.5).to(dtype)
+    b = (torch.randn(out_features, generator=g) * 0.5).to(dtype) if bias else None
+    with torch.inference_mode():
+        fn = linear_gelu if gelu else linear
+        y = fn(x.cuda(), w.cuda(), None if b is None else b.cuda())
+    assert y.shape == (rows, out_features)
+    _check(y, _reference(x, w, b, gelu), dtype)

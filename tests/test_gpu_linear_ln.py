@@ -23,6 +23,8 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -241,3 +243,30 @@ def test_rejects_what_it_cannot_run(gpu_ready):
         linear_residual_layer_norm(a[:, :192], wp, b, x, gamma, beta, 1e-5)
     with pytest.raises(ValueError, match="dtype"):
         linear_residual_layer_norm(a.float(), wp, b, x, gamma, beta, 1e-5)
+
+
+@pytest.mark.parametrize("case_seed", range(8))
+def test_random_shapes_against_unfused_route(gpu_ready, case_seed):
+    # Seeded sweep: M from 1 to 2500 (ragged row blocks), K a multiple of 128
+    # up to 2048, bias and LayerNorm bias present or not, both dtypes, both
+    # the default and the hand-over route (the same bits).
+    from transformer_opt.kernels.linear_ln import linear_residual_layer_norm, pack_weight
+
+    rng = np.random.default_rng(2000 + case_seed)
+    rows = int(rng.integers(1, 2501))
+    in_features = 128 * int(rng.integers(1, 17))
+    dtype = (torch.bfloat16, torch.float16)[case_seed % 2]
+    bias, ln_bias = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    a, w, b, x, gamma, beta = _inputs(rows, in_features, dtype, 7 * case_seed + 1, bias, ln_bias)
+    with torch.inference_mode():
+        wp = pack_weight(w)
+        r, y = linear_residual_layer_norm(a, wp, b, x, gamma, beta, 1e-5)
+        r1, y1 = linear_residual_layer_norm(a, wp, b, x, gamma, beta, 1e-5, max_polls=0)
+    assert torch.equal(r, r1) and torch.equal(y, y1)
+    if in_features >= 256:  # the comparison route's linear kernel takes K >= 256
+        _check_against_unfused(a, w, b, x, gamma, beta, 1e-5, r, y)
+    else:
+        q = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+        y64 = _layer_norm64(r, gamma, beta, 1e-5)
+        err = (y.double().cpu() - y64).abs()
+        assert bool((err <= q * y64.abs() + 1e-5 * (1 + gamma.double().abs().max().item())).all())
